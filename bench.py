@@ -1,0 +1,292 @@
+#!/usr/bin/env python3
+"""Benchmark of the PageGauge INT8 paged decode on one MI355X.
+
+Metric: B1/49K INT8 paged-decode microseconds per call and the
+fraction of the HBM roofline.  Workload: one request of 49152 tokens (3056
+INT8 page-affine pages + a 256-token FP16 exact tail), Mistral-7B layer shape
+(32 query / 8 KV heads, head_dim 128, 16-token pages), seeded N(0,1) K/V with
+x8 on 4 of 128 channels, randomly permuted physical page table.
+
+A step is one decode call: the INT8+tail partial kernel and the combine kernel
+(value center and base-2 LSE included).  Following the reference protocol
+(scripts/benchmark_flashinfer_page_affine_int8.py:295-349, :651-655) each
+cold sample is preceded by an untimed HBM scrub (256 MiB, and a 1 GiB
+variant because MI355X's 256 MB Infinity Cache holds the whole working set);
+hot samples run back to back.  HIP events on the launch stream bracket the
+partial kernel (the roofline's dominant kernel) and the whole call.
+
+Also reported: the same-way FP16 paged-decode kernel on an FP16 copy of the
+same cache, and the CPU baseline (the C oracle's dense decode of the same
+inputs, one host thread).  Prints one JSON line.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import statistics
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+if str(ROOT) not in sys.path:
+    sys.path.insert(0, str(ROOT))
+
+HBM_PEAK_GBPS = 8000.0
+
+
+def parse_args() -> argparse.Namespace:
+    p = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
+    p.add_argument("--gpus", type=int, default=1)
+    p.add_argument("--steps", type=int, default=100, help="timed cold decode calls")
+    p.add_argument("--warmup", type=int, default=10)
+    p.add_argument("--seed", type=int, default=20260840)
+    p.add_argument("--scrub-mib", type=int, default=256)
+    p.add_argument("--big-scrub-mib", type=int, default=1024)
+    p.add_argument("--hot-repeats", type=int, default=200)
+    p.add_argument("--split", type=int, default=0, help="pages per work item (0 = scheduler)")
+    p.add_argument("--cpu-seconds", type=float, default=12.0, help="CPU-baseline time budget")
+    p.add_argument("--no-cpu", action="store_true")
+    p.add_argument("--no-fp16", action="store_true")
+    p.add_argument("--sweep", default="", help="comma list of split sizes to time (pilot sweep)")
+    return p.parse_args()
+
+
+def summarize(values_ms):
+    ordered = sorted(values_ms)
+    n = len(ordered)
+    return {
+        "p50_us": 1e3 * statistics.median(ordered),
+        "p05_us": 1e3 * ordered[round(0.05 * (n - 1))],
+        "p95_us": 1e3 * ordered[round(0.95 * (n - 1))],
+        "mean_us": 1e3 * statistics.fmean(ordered),
+        "min_us": 1e3 * ordered[0],
+        "samples": n,
+    }
+
+
+def timed_calls(torch, bound, n, scrub=None):
+    """Per-call HIP events: (partial kernel ms list, whole call ms list).
+
+    ``scrub`` runs before every sample, outside the events; it also keeps the
+    GPU busy while the host queues the timed launches.
+    """
+    ev = [[torch.cuda.Event(enable_timing=True) for _ in range(3)] for _ in range(n)]
+    for i in range(n):
+        if scrub is not None:
+            scrub()
+        ev[i][0].record()
+        bound.partial()
+        ev[i][1].record()
+        bound.combine()
+        ev[i][2].record()
+    torch.cuda.synchronize()
+    kernel = [a.elapsed_time(b) for a, b, _ in ev]
+    call = [a.elapsed_time(c) for a, _, c in ev]
+    return kernel, call
+
+
+def measure(torch, bound, args, scrub_small, scrub_big):
+    for _ in range(args.warmup):
+        scrub_small()
+        bound()
+    torch.cuda.synchronize()
+    cold_k, cold_c = timed_calls(torch, bound, args.steps, scrub=scrub_small)
+    big_n = max(10, args.steps // 4)
+    big_k, big_c = timed_calls(torch, bound, big_n, scrub=scrub_big)
+    # hot: back-to-back calls (no events in between) after a long head-start
+    # kernel; per-call time = span / repeats
+    hot = []
+    for _ in range(5):
+        start = torch.cuda.Event(enable_timing=True)
+        end = torch.cuda.Event(enable_timing=True)
+        scrub_big()
+        bound()
+        start.record()
+        for _ in range(args.hot_repeats):
+            bound()
+        end.record()
+        torch.cuda.synchronize()
+        hot.append(start.elapsed_time(end) / args.hot_repeats)
+    return {
+        "cold_256mib": {"kernel": summarize(cold_k), "call": summarize(cold_c)},
+        "cold_1gib": {"kernel": summarize(big_k), "call": summarize(big_c)},
+        "hot": {"call": summarize(hot), "repeats_per_sample": args.hot_repeats},
+        "_cold_kernel_ms": cold_k,
+        "_cold_call_ms": cold_c,
+    }
+
+
+def cpu_baseline(w, budget_s: float):
+    """C oracle dense decode of the same inputs, one host thread."""
+    from oracle import c_oracle
+
+    c = lambda t: t.detach().cpu().numpy()  # noqa: E731
+    host = dict(query=c(w.query), k_codes=c(w.k_codes), v_codes=c(w.v_codes), k_scale=c(w.k_scale),
+                v_scale=c(w.v_scale), indptr=c(w.old_indptr), indices=c(w.old_indices),
+                last_page_len=c(w.old_last_page_len), sm_scale=w.sm_scale, tail_k=c(w.tail_k),
+                tail_v=c(w.tail_v), tail_indptr=c(w.tail_indptr), tail_indices=c(w.tail_indices),
+                tail_last_len=c(w.tail_last_page_len), value_center=c(w.value_center))
+    times = []
+    out = lse = None
+    start = time.perf_counter()
+    while True:
+        t0 = time.perf_counter()
+        out, lse = c_oracle.decode_page_gauge(**host)
+        times.append(time.perf_counter() - t0)
+        if time.perf_counter() - start >= budget_s or len(times) >= 200:
+            break
+    return times, out, lse
+
+
+def main() -> int:
+    args = parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU only (the path is a single-GPU decode; sharding is "
+              f"described in DESIGN.md); --gpus {args.gpus} is not supported", file=sys.stderr)
+        return 2
+    import numpy as np
+    import torch
+
+    from pagegauge_amd import decode, workloads
+
+    if not torch.cuda.is_available():
+        print("bench.py needs a GPU", file=sys.stderr)
+        return 1
+    device = torch.device("cuda:0")
+    torch.cuda.set_device(device)
+    t_setup = time.perf_counter()
+    w = workloads.b1_49k(args.seed, device=device, with_fp16_copy=not args.no_fp16)
+    torch.cuda.synchronize()
+    setup_s = time.perf_counter() - t_setup
+
+    workspace = torch.empty(64 << 20, dtype=torch.uint8, device=device)
+    out = torch.empty_like(w.query)
+    lse = torch.empty(w.batch, 32, dtype=torch.float32, device=device)
+    dec = decode.PageGaugeSegmentedDecode(workspace)
+    dec.plan(w.old_indptr, w.old_indices, w.old_last_page_len, w.tail_indptr, w.tail_indices,
+             w.tail_last_page_len, fixed_split_size=args.split or None)
+    bound = dec.bind(w.query, (w.k_codes, w.v_codes), w.k_scale, w.v_scale, (w.tail_k, w.tail_v),
+                     w.value_center, out=out, lse=lse)
+
+    scrub_small_buf = torch.zeros(args.scrub_mib * (1 << 20) // 4, dtype=torch.int32, device=device)
+    scrub_big_buf = torch.zeros(args.big_scrub_mib * (1 << 20) // 4, dtype=torch.int32, device=device)
+    scrub_small = lambda: scrub_small_buf.add_(1)  # noqa: E731
+    scrub_big = lambda: scrub_big_buf.add_(1)  # noqa: E731
+
+    # contract timed region: K cold steps bracketed by synchronize
+    torch.cuda.synchronize()
+    wall0 = time.perf_counter()
+    int8 = measure(torch, bound, args, scrub_small, scrub_big)
+    torch.cuda.synchronize()
+    wall_s = time.perf_counter() - wall0
+    bound()
+    torch.cuda.synchronize()
+    gpu_out = out.detach().cpu().numpy()
+    gpu_lse = lse.detach().cpu().numpy()
+
+    alg_bytes = w.algorithmic_bytes()
+    kernel_mean_us = int8["cold_256mib"]["kernel"]["mean_us"]
+    call_p50_us = int8["cold_256mib"]["call"]["p50_us"]
+    achieved = alg_bytes / (kernel_mean_us * 1e-6) / 1e9
+
+    fp16 = None
+    if not args.no_fp16:
+        ws16 = torch.empty(64 << 20, dtype=torch.uint8, device=device)
+        out16 = torch.empty_like(w.query)
+        lse16 = torch.empty_like(lse)
+        wrap16 = decode.BatchDecodeWithPagedKVCacheWrapper(ws16, "NHD")
+        wrap16.plan(w.fp16_indptr, w.fp16_indices, w.fp16_last_page_len, 32, 8, 128, 16,
+                    kv_data_type=torch.float16, fixed_split_size=None)
+        bound16 = wrap16.bind(w.query, (w.fp16_k, w.fp16_v), out=out16, lse=lse16)
+        fp16 = measure(torch, bound16, args, scrub_small, scrub_big)
+        fp16_bytes = w.fp16_algorithmic_bytes()
+        fp16["algorithmic_bytes"] = fp16_bytes
+        fp16["split_pages"] = wrap16.split_pages
+        fp16["achieved_gbps_cold_kernel"] = fp16_bytes / (fp16["cold_256mib"]["kernel"]["mean_us"] * 1e-6) / 1e9
+
+    sweep = {}
+    for item in [s for s in args.sweep.split(",") if s.strip()]:
+        split = int(item)
+        d2 = decode.PageGaugeSegmentedDecode(workspace)
+        d2.plan(w.old_indptr, w.old_indices, w.old_last_page_len, w.tail_indptr, w.tail_indices,
+                w.tail_last_page_len, fixed_split_size=split)
+        b2 = d2.bind(w.query, (w.k_codes, w.v_codes), w.k_scale, w.v_scale, (w.tail_k, w.tail_v),
+                     w.value_center, out=out, lse=lse)
+        k_ms, c_ms = timed_calls(torch, b2, max(20, args.steps // 2), scrub=scrub_small)
+        sweep[str(split)] = {"items": d2.num_work_items, "kernel_p50_us": 1e3 * statistics.median(k_ms),
+                             "call_p50_us": 1e3 * statistics.median(c_ms)}
+
+    cpu = None
+    parity = None
+    if not args.no_cpu:
+        times, ref_out, ref_lse = cpu_baseline(w, args.cpu_seconds)
+        cpu = {
+            "value": 1e6 * statistics.median(times),
+            "unit": "us/call",
+            "cores": 1,
+            "kind": "port",
+            "sample": (f"full B1/49K decode of the same inputs (3056 INT8 + 16 FP16 pages, "
+                       f"dense float32, C oracle, one thread), {len(times)} calls"),
+        }
+        parity = {
+            "oracle": "C oracle dense float32 decode",
+            "max_abs_out": float(np.abs(gpu_out.astype(np.float64) - ref_out.astype(np.float64)).max()),
+            "max_abs_lse": float(np.abs(gpu_lse.astype(np.float64) - ref_lse.astype(np.float64)).max()),
+            "tolerance_out": 2e-3,
+        }
+
+    result = {
+        "metric": "B1/49K INT8 paged-decode us/call (cold, 256 MiB scrub; whole call incl. combine)",
+        "value": round(call_p50_us, 3),
+        "unit": "us/call",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(call_p50_us / 1e3, 6),
+        "higher_is_better": False,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "int8 codes (int32 MFMA accumulate) + fp16 tail, fp32 softmax",
+        "data": "synthetic (seeded N(0,1) K/V, x8 outliers on 4/128 channels, permuted page table)",
+        "config": {
+            "workload": "b1_49k: B=1, 49152 tokens = 3056 INT8 pages + 16 FP16 tail pages, "
+                        "Hq=32 Hkv=8 D=128 page 16",
+            "seed": args.seed,
+            "split_pages": dec.split_pages,
+            "tail_split_pages": dec.tail_split_pages,
+            "work_items": dec.num_work_items,
+            "step": "one decode call (partial kernel + combine kernel) after an untimed HBM scrub",
+        },
+        "roofline": {
+            "bound": "hbm",
+            "kernel": "decode_partial_kernel",
+            "achieved": round(achieved, 1),
+            "peak": HBM_PEAK_GBPS,
+            "unit": "GB/s",
+            "frac": round(achieved / HBM_PEAK_GBPS, 4),
+            "traffic": None,
+            "algorithmic_bytes": alg_bytes,
+            "kernel_mean_us": round(kernel_mean_us, 3),
+        },
+        "cpu_baseline": cpu,
+        "timings_int8": {k: v for k, v in int8.items() if not k.startswith("_")},
+        "timings_fp16_same_way": None if fp16 is None else {k: v for k, v in fp16.items() if not k.startswith("_")},
+        "speedup_vs_fp16_same_way": None if fp16 is None else {
+            mode: round(fp16[mode]["call"]["p50_us"] / int8[mode]["call"]["p50_us"], 4)
+            for mode in ("cold_256mib", "cold_1gib", "hot")},
+        "parity_vs_oracle": parity,
+        "split_sweep": sweep or None,
+        "wall_s_timed_region": round(wall_s, 3),
+        "setup_s": round(setup_s, 2),
+        "device": torch.cuda.get_device_name(device),
+        "host_cpus": os.cpu_count(),
+    }
+    print(json.dumps(result), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

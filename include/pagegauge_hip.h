@@ -1,0 +1,263 @@
+/*
+ * pagegauge_hip.h -- C ABI of libpagegauge_hip.so, the MI355X (gfx950)
+ * implementation of PageGauge's compressed-KV decode path.
+ *
+ * Plain pointers and sizes only.  Every pointer argument is device memory
+ * unless its name starts with ``host_``; ``stream`` is a hipStream_t passed as
+ * void* (NULL = the null stream).  Every function returns PG_OK (0) or an
+ * error code; pg_last_error() then gives the message of the failing call on
+ * the calling thread.  No entry point allocates device memory, synchronises
+ * the stream or returns data to the host except pg_decode_plan (which copies
+ * a work list into the caller's workspace and waits for that copy).
+ *
+ * Layouts (reference conventions, tests/page_gauge_append_extension.cu:1-40):
+ *   query / key / value rows   fp16 [B, H, 128] with contiguous head rows,
+ *                              batch stride given in elements
+ *   FP16 and INT8 page caches  NHD [pages, 16, Hkv, 128]
+ *   page scales                fp16 [pages, Hkv]
+ *   centers                    fp16 [B, Hkv, 128] (or [Hkv, 128] when B == 1)
+ *   lse                        float32 [B, Hq], base 2 (log2-sum-exp2 of
+ *                              sm_scale*log2(e)*q.k)
+ */
+#ifndef PAGEGAUGE_HIP_H
+#define PAGEGAUGE_HIP_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum {
+  PG_OK = 0,
+  PG_ERROR_INVALID_ARGUMENT = 1,
+  PG_ERROR_LAUNCH = 2,
+  PG_ERROR_UNSUPPORTED = 3,
+  PG_ERROR_WORKSPACE = 4
+};
+
+/* Message of the last failing call on this thread ("" if none). */
+const char* pg_last_error(void);
+/* ABI version of this library (increments on incompatible changes). */
+int32_t pg_abi_version(void);
+
+/* ------------------------------------------------------------------------
+ * Cache update (K2).  Replaces the pybind entry points of
+ * tests/page_gauge_append_extension.cu:1030-1040.
+ * ---------------------------------------------------------------------- */
+
+/* Fused RoPE + FP16 NHD append.  Replaces rope_append_fp16
+ * (tests/page_gauge_append_extension.cu:644-685) when device_position is NULL
+ * (position = host_position, cosine/sine are the [128] rows of that
+ * position) and rope_append_fp16_dynamic (:687-745) otherwise (position read
+ * on the device from device_position[0]; cosine/sine are [rope_rows, 128]
+ * tables with row stride rope_row_stride).  Writes rotated_query [B,Hq,128]
+ * and row (position % 16) of physical page request*pages_per_request +
+ * position/16.  A position outside the cache (or the RoPE table) is a no-op,
+ * as in the reference kernel (:202-207). */
+int32_t pg_rope_append_fp16(const void* query, const void* key, const void* value,
+                            const void* cosine, const void* sine, void* rotated_query,
+                            void* key_pages, void* value_pages,
+                            int64_t query_batch_stride, int64_t key_batch_stride,
+                            int64_t value_batch_stride, int32_t batch_size,
+                            int32_t query_heads, int32_t kv_heads,
+                            int32_t pages_per_request, int32_t host_position,
+                            const int32_t* device_position, int64_t rope_row_stride,
+                            int32_t rope_rows, void* stream);
+
+/* Fused RoPE + centered K/V append into the FP16 exact ring + completed-page
+ * INT8 finalize.  Replaces rope_append_page_gauge
+ * (tests/page_gauge_append_extension.cu:747-836, device_position == NULL)
+ * and rope_append_page_gauge_dynamic (:838-948).  Ring slot of logical page p
+ * is request*exact_pages_per_request + (p < sink ? p : sink + p % (E - sink));
+ * on the page's last token the page is quantised into code page
+ * request*code_pages_per_request + p and scale row of that code page.
+ * center_batch_stride is Hkv*128 for [B,Hkv,128] centers, 0 for [Hkv,128]. */
+int32_t pg_rope_append_page_gauge(const void* query, const void* key, const void* value,
+                                  const void* cosine, const void* sine,
+                                  const void* key_center, const void* value_center,
+                                  int64_t center_batch_stride, void* rotated_query,
+                                  void* exact_key_pages, void* exact_value_pages,
+                                  int8_t* key_codes, int8_t* value_codes,
+                                  void* key_scales, void* value_scales,
+                                  int64_t query_batch_stride, int64_t key_batch_stride,
+                                  int64_t value_batch_stride, int32_t batch_size,
+                                  int32_t query_heads, int32_t kv_heads,
+                                  int32_t exact_pages_per_request, int32_t exact_sink_pages,
+                                  int32_t code_pages_per_request, int32_t host_position,
+                                  const int32_t* device_position, int64_t rope_row_stride,
+                                  int32_t rope_rows, void* stream);
+
+/* Per-request-position variant of pg_rope_append_page_gauge (no reference
+ * counterpart in the CUDA extension; the per-request page semantics follow
+ * the Triton append_finalize_page_gauge,
+ * scripts/benchmark_page_gauge_overheads.py:112-205).  Request r uses
+ * position positions[r] (device int32 [B]) and RoPE row positions[r] of the
+ * [rope_rows, 128] tables; each row behaves exactly as the scalar kernel. */
+int32_t pg_rope_append_page_gauge_positions(
+    const void* query, const void* key, const void* value, const void* cosine,
+    const void* sine, const int32_t* positions, const void* key_center,
+    const void* value_center, int64_t center_batch_stride, void* rotated_query,
+    void* exact_key_pages, void* exact_value_pages, int8_t* key_codes,
+    int8_t* value_codes, void* key_scales, void* value_scales,
+    int64_t query_batch_stride, int64_t key_batch_stride, int64_t value_batch_stride,
+    int32_t batch_size, int32_t query_heads, int32_t kv_heads,
+    int32_t exact_pages_per_request, int32_t exact_sink_pages,
+    int32_t code_pages_per_request, int64_t rope_row_stride, int32_t rope_rows,
+    void* stream);
+
+/* Per-request FP16 append at (page_ids[r], page_offsets[r]).  Replaces the
+ * Triton append_kv (scripts/benchmark_page_gauge_overheads.py:86-109,
+ * :242-269).  key/value contiguous [B, H, 128]. */
+int32_t pg_append_kv(const void* key, const void* value, void* key_pages, void* value_pages,
+                     const int32_t* page_ids, const int32_t* page_offsets,
+                     int32_t batch_size, int32_t heads, int32_t num_pages, void* stream);
+
+/* Per-request centered append + completed-page finalize without RoPE.
+ * Replaces the Triton append_finalize_page_gauge
+ * (scripts/benchmark_page_gauge_overheads.py:112-205, :272-317).  Exact and
+ * code caches share page indices; centers are [H,128]. */
+int32_t pg_append_finalize_page_gauge(const void* key, const void* value,
+                                      const void* key_center, const void* value_center,
+                                      void* exact_key_pages, void* exact_value_pages,
+                                      int8_t* key_codes, int8_t* value_codes,
+                                      void* key_scales, void* value_scales,
+                                      const int32_t* page_ids, const int32_t* page_offsets,
+                                      int32_t batch_size, int32_t heads, int32_t num_pages,
+                                      void* stream);
+
+/* Bulk completed-page quantizer.  Replaces the Triton
+ * quantize_completed_kv_pages (scripts/benchmark_page_gauge_overheads.py:23-83,
+ * :208-239): float32-centered values, scale fp16(max(amax/127, 2^-20)),
+ * sign-symmetric floor(q+0.5) codes.  key/value [pages,16,H,128] fp16,
+ * centers [H,128]. */
+int32_t pg_quantize_completed_kv_pages(const void* key, const void* value,
+                                       const void* key_center, const void* value_center,
+                                       int8_t* key_codes, int8_t* value_codes,
+                                       void* key_scales, void* value_scales,
+                                       int64_t num_pages, int32_t heads, void* stream);
+
+/* ------------------------------------------------------------------------
+ * Paged decode (K1) and the split scheduler (S).
+ * ---------------------------------------------------------------------- */
+
+/* Host-side description of a planned decode; filled by pg_decode_plan and
+ * passed unchanged to pg_decode_run.  Plain data, safe to copy. */
+typedef struct pg_decode_plan {
+  int32_t batch_size;
+  int32_t num_qo_heads;
+  int32_t num_kv_heads;
+  int32_t head_dim;
+  int32_t page_size;
+  int32_t primary_kind;   /* PG_KV_INT8 or PG_KV_FP16: element type of segment 0 */
+  int32_t has_tail;       /* 1 if an FP16 tail segment joins the softmax */
+  int32_t split_pages;    /* pages per work item, segment 0 */
+  int32_t tail_split_pages;
+  int32_t num_items;      /* work items (one workgroup each) */
+  int32_t num_items_primary;
+  int32_t max_items_per_request;
+  int64_t items_offset;   /* byte offsets inside the workspace */
+  int64_t item_ptr_offset;
+  int64_t partial_offset;
+  int64_t workspace_bytes;
+} pg_decode_plan_t;
+
+enum { PG_KV_INT8 = 0, PG_KV_FP16 = 1 };
+
+/* Bytes of workspace a plan with these bounds needs. */
+int64_t pg_decode_workspace_bytes(int32_t batch_size, int32_t num_qo_heads,
+                                  int64_t max_items);
+
+/* Split-count selection for 256-CU MI355X: pages per work item such that the
+ * whole launch fills the GPU in (close to) whole waves of workgroups.
+ * Replaces FlashInfer's automatic split (fixed_split_size=None) and the
+ * capacity bound (2*num_SMs)//Hkv of
+ * diagnostics/benchmark_sustained_dynamic_graphs.py:1497-1534.  bytes_per_page
+ * is the per-(page, kv head) K+V traffic (4096 for INT8, 8192 for FP16). */
+int32_t pg_select_split_pages(int64_t total_pages, int32_t batch_size, int32_t num_kv_heads,
+                              int32_t bytes_per_page, int32_t num_cus);
+
+/* Plan a decode.  host_indptr [B+1] / host_last_page_len [B]: segment 0
+ * (INT8 codes or FP16 pages, primary_kind); host_tail_indptr/_last_len: the
+ * optional FP16 tail segment (NULL if none).  split_pages / tail_split_pages
+ * <= 0 select automatically (pg_select_split_pages).  Writes the work list
+ * into the device workspace (synchronous copy on ``stream``).  Replaces
+ * BatchDecodeWithPagedKVCacheWrapper.plan as called by
+ * scripts/benchmark_flashinfer_page_affine_int8.py:363-389. */
+int32_t pg_decode_plan(const int32_t* host_indptr, const int32_t* host_last_page_len,
+                       int32_t batch_size, int32_t primary_kind,
+                       const int32_t* host_tail_indptr, const int32_t* host_tail_last_len,
+                       int32_t num_qo_heads, int32_t num_kv_heads, int32_t head_dim,
+                       int32_t page_size, int32_t split_pages, int32_t tail_split_pages,
+                       int32_t num_cus, void* workspace, int64_t workspace_bytes,
+                       pg_decode_plan_t* plan, void* stream);
+
+/* Run a planned decode.  Segment 0: pages ``indices`` (indptr/last_page_len
+ * as planned; last_page_len is re-read on the device every call, so a
+ * caller may advance it without re-planning) of k_cache/v_cache, which are
+ * INT8 codes with k_scale/v_scale [N,Hkv] for PG_KV_INT8 or FP16 pages
+ * (scales NULL) for PG_KV_FP16.  Tail segment (if planned): FP16 centered
+ * ring pages tail_k/tail_v through tail_indices.  value_center (may be NULL)
+ * is added once after normalisation, repeated over the GQA group.  Writes
+ * out fp16 [B,Hq,128] and, if lse != NULL, base-2 lse [B,Hq].
+ * Replaces the patched FlashInfer run (int8 patch, prefill.cuh), FlashInfer's
+ * split merge, the tail decode, merge_state_in_place and add_(output_center)
+ * of scripts/benchmark_flashinfer_page_affine_int8.py:566-602, or the
+ * heterogeneous one-launch run (scripts/page_gauge_heterogeneous_fa2.py:355-381).
+ * GQA group size must be 4 and head_dim 128. */
+int32_t pg_decode_run(const pg_decode_plan_t* plan, const void* query,
+                      int64_t query_batch_stride, const void* k_cache, const void* v_cache,
+                      const void* k_scale, const void* v_scale, const int32_t* indices,
+                      const int32_t* last_page_len, const void* tail_k, const void* tail_v,
+                      const int32_t* tail_indices, const int32_t* tail_last_len,
+                      const void* value_center, int64_t center_batch_stride, void* out,
+                      float* lse, float sm_scale, void* workspace, void* stream);
+
+/* The two launches of pg_decode_run, for callers that schedule them
+ * separately (e.g. to time the partial kernel, or to overlap the combine
+ * with other work): pg_decode_run_partial writes one unnormalised partial
+ * (o[128], m, l) per work item and query head into the workspace;
+ * pg_decode_run_combine merges each request's partials (base-2 LSE merge),
+ * normalises, adds value_center and writes out/lse.  Together they are
+ * exactly pg_decode_run.  These replace FlashInfer's split-KV decode kernel
+ * and its VariableLengthMergeStates merge (plan fields merge_indptr /
+ * block_valid_mask, scripts/benchmark_page_gauge_transformer.py:1401-1416). */
+int32_t pg_decode_run_partial(const pg_decode_plan_t* plan, const void* query,
+                              int64_t query_batch_stride, const void* k_cache,
+                              const void* v_cache, const void* k_scale, const void* v_scale,
+                              const int32_t* indices, const int32_t* last_page_len,
+                              const void* tail_k, const void* tail_v, const int32_t* tail_indices,
+                              const int32_t* tail_last_len, float sm_scale, void* workspace,
+                              void* stream);
+int32_t pg_decode_run_combine(const pg_decode_plan_t* plan, const void* value_center,
+                              int64_t center_batch_stride, void* out, float* lse,
+                              void* workspace, void* stream);
+
+/* Base-2 LSE state merge in place: v, s <- merge((v, s), (v_other, s_other)).
+ * Replaces flashinfer.merge_state_in_place as used by
+ * scripts/benchmark_flashinfer_page_affine_int8.py:598-600.  v [rows, heads,
+ * head_dim] fp16 contiguous, s [rows, heads] float32; mask (uint8 [rows] or
+ * NULL): rows with mask 0 are left unchanged. */
+int32_t pg_merge_state_in_place(void* v, float* s, const void* v_other, const float* s_other,
+                                const uint8_t* mask, int32_t rows, int32_t heads,
+                                int32_t head_dim, void* stream);
+
+/* Fused exact-tail attention + state merge + value-center restore.  Replaces
+ * exact_tail_merge_center (tests/page_gauge_append_extension.cu:950-1028).
+ * query [B,Hq,128] contiguous; tail of request r = (n-1)*16 +
+ * exact_last_page_len[r] tokens through exact_page_indices[r*n .. r*n+n-1]
+ * (1 <= n <= 16); old_output/old_lse updated in place. */
+int32_t pg_exact_tail_merge_center(const void* query, const void* exact_key_pages,
+                                   const void* exact_value_pages,
+                                   const int32_t* exact_page_indices,
+                                   const int32_t* exact_last_page_len, void* old_output,
+                                   float* old_lse, const void* value_center,
+                                   int64_t center_batch_stride, int32_t batch_size,
+                                   int32_t query_heads, int32_t kv_heads,
+                                   int32_t pages_per_request, float sm_scale, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* PAGEGAUGE_HIP_H */

@@ -1,0 +1,123 @@
+"""ctypes binding of ``libpagegauge_hip.so`` (C ABI: ``include/pagegauge_hip.h``).
+
+The library is built in-tree by ``pagegauge_amd/build.py`` (``__graft_entry__.build``).
+There is no fallback: if the library is missing or cannot be loaded every
+operator raises, so a GPU run can never silently use another path.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import threading
+from pathlib import Path
+
+LIBRARY_PATH = Path(__file__).resolve().parent / "lib" / "libpagegauge_hip.so"
+ABI_VERSION = 1
+
+PG_OK = 0
+PG_KV_INT8 = 0
+PG_KV_FP16 = 1
+
+_p = ctypes.c_void_p
+_i32 = ctypes.c_int32
+_i64 = ctypes.c_int64
+_f32 = ctypes.c_float
+
+
+class DecodePlan(ctypes.Structure):
+    """Mirror of ``pg_decode_plan_t``."""
+
+    _fields_ = [
+        ("batch_size", _i32),
+        ("num_qo_heads", _i32),
+        ("num_kv_heads", _i32),
+        ("head_dim", _i32),
+        ("page_size", _i32),
+        ("primary_kind", _i32),
+        ("has_tail", _i32),
+        ("split_pages", _i32),
+        ("tail_split_pages", _i32),
+        ("num_items", _i32),
+        ("num_items_primary", _i32),
+        ("max_items_per_request", _i32),
+        ("items_offset", _i64),
+        ("item_ptr_offset", _i64),
+        ("partial_offset", _i64),
+        ("workspace_bytes", _i64),
+    ]
+
+
+# name -> (restype, argtypes); every symbol declared in include/pagegauge_hip.h
+PROTOTYPES = {
+    "pg_last_error": (ctypes.c_char_p, []),
+    "pg_abi_version": (_i32, []),
+    "pg_rope_append_fp16": (_i32, [_p, _p, _p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _i32, _i32,
+                                   _i32, _i32, _i32, _p, _i64, _i32, _p]),
+    "pg_rope_append_page_gauge": (_i32, [_p, _p, _p, _p, _p, _p, _p, _i64, _p, _p, _p, _p, _p, _p,
+                                         _p, _i64, _i64, _i64, _i32, _i32, _i32, _i32, _i32, _i32,
+                                         _i32, _p, _i64, _i32, _p]),
+    "pg_rope_append_page_gauge_positions": (_i32, [_p, _p, _p, _p, _p, _p, _p, _p, _i64, _p, _p,
+                                                   _p, _p, _p, _p, _p, _i64, _i64, _i64, _i32,
+                                                   _i32, _i32, _i32, _i32, _i32, _i64, _i32, _p]),
+    "pg_append_kv": (_i32, [_p, _p, _p, _p, _p, _p, _i32, _i32, _i32, _p]),
+    "pg_append_finalize_page_gauge": (_i32, [_p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _i32,
+                                             _i32, _i32, _p]),
+    "pg_quantize_completed_kv_pages": (_i32, [_p, _p, _p, _p, _p, _p, _p, _p, _i64, _i32, _p]),
+    "pg_decode_workspace_bytes": (_i64, [_i32, _i32, _i64]),
+    "pg_select_split_pages": (_i32, [_i64, _i32, _i32, _i32, _i32]),
+    "pg_decode_plan": (_i32, [_p, _p, _i32, _i32, _p, _p, _i32, _i32, _i32, _i32, _i32, _i32,
+                              _i32, _p, _i64, ctypes.POINTER(DecodePlan), _p]),
+    "pg_decode_run": (_i32, [ctypes.POINTER(DecodePlan), _p, _i64, _p, _p, _p, _p, _p, _p, _p, _p,
+                             _p, _p, _p, _i64, _p, _p, _f32, _p, _p]),
+    "pg_decode_run_partial": (_i32, [ctypes.POINTER(DecodePlan), _p, _i64, _p, _p, _p, _p, _p, _p,
+                                     _p, _p, _p, _p, _f32, _p, _p]),
+    "pg_decode_run_combine": (_i32, [ctypes.POINTER(DecodePlan), _p, _i64, _p, _p, _p, _p]),
+    "pg_merge_state_in_place": (_i32, [_p, _p, _p, _p, _p, _i32, _i32, _i32, _p]),
+    "pg_exact_tail_merge_center": (_i32, [_p, _p, _p, _p, _p, _p, _p, _p, _i64, _i32, _i32, _i32,
+                                          _i32, _f32, _p]),
+}
+
+_lock = threading.Lock()
+_library = None
+
+
+class LibraryMissingError(RuntimeError):
+    pass
+
+
+def library():
+    """Load (once) and return the ctypes handle; raises if the build is absent."""
+    global _library
+    if _library is not None:
+        return _library
+    with _lock:
+        if _library is None:
+            if not LIBRARY_PATH.exists():
+                raise LibraryMissingError(
+                    f"{LIBRARY_PATH} is missing: build it with `python -c "
+                    "'import __graft_entry__ as g; g.build()'` (hipcc, gfx950)")
+            lib = ctypes.CDLL(str(LIBRARY_PATH))
+            for name, (restype, argtypes) in PROTOTYPES.items():
+                fn = getattr(lib, name)
+                fn.restype = restype
+                fn.argtypes = argtypes
+            version = lib.pg_abi_version()
+            if version != ABI_VERSION:
+                raise LibraryMissingError(
+                    f"libpagegauge_hip.so ABI {version} does not match the bindings ({ABI_VERSION})")
+            _library = lib
+    return _library
+
+
+def last_error() -> str:
+    return library().pg_last_error().decode("utf-8", "replace")
+
+
+def check(rc: int, what: str) -> None:
+    """Raise RuntimeError carrying the library's message for a failing call."""
+    if rc != PG_OK:
+        raise RuntimeError(f"{what}: {last_error()} (code {rc})")
+
+
+def call(name: str, *args) -> None:
+    check(getattr(library(), name)(*args), name)

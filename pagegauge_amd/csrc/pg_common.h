@@ -1,0 +1,69 @@
+// Shared definitions of the PageGauge MI355X (gfx950) library.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <hip/hip_fp16.h>
+#include <stdint.h>
+
+#include <string>
+
+#include "../../include/pagegauge_hip.h"
+
+namespace pg {
+
+constexpr int kHeadDim = 128;
+constexpr int kPageSize = 16;
+constexpr int kWave = 64;
+constexpr int kGqa = 4;  // query heads per KV head handled by the decode kernels
+
+// Records the message of a failing call for pg_last_error().
+void set_error(const std::string& message);
+void clear_error();
+
+inline int32_t fail(int32_t code, const std::string& message) {
+  set_error(message);
+  return code;
+}
+
+inline int32_t check_launch(const char* what) {
+  hipError_t status = hipGetLastError();
+  if (status != hipSuccess) {
+    return fail(PG_ERROR_LAUNCH, std::string(what) + ": " + hipGetErrorString(status));
+  }
+  return PG_OK;
+}
+
+inline hipStream_t as_stream(void* stream) { return reinterpret_cast<hipStream_t>(stream); }
+
+// -- device helpers ------------------------------------------------------
+
+__device__ __forceinline__ float half_bits_to_float(uint16_t bits) {
+  return __half2float(__ushort_as_half(bits));
+}
+
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+  for (int offset = 32; offset > 0; offset >>= 1) v = fmaxf(v, __shfl_xor(v, offset, kWave));
+  return v;
+}
+
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int offset = 32; offset > 0; offset >>= 1) v += __shfl_xor(v, offset, kWave);
+  return v;
+}
+
+// Reductions over the 16 lanes of one DPP row (lanes 16*r .. 16*r+15).
+__device__ __forceinline__ float row16_max(float v) {
+#pragma unroll
+  for (int offset = 8; offset > 0; offset >>= 1) v = fmaxf(v, __shfl_xor(v, offset, kWave));
+  return v;
+}
+
+__device__ __forceinline__ float row16_sum(float v) {
+#pragma unroll
+  for (int offset = 8; offset > 0; offset >>= 1) v += __shfl_xor(v, offset, kWave);
+  return v;
+}
+
+}  // namespace pg
