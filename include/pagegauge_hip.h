@@ -164,9 +164,10 @@ typedef struct pg_decode_plan {
 
 enum { PG_KV_INT8 = 0, PG_KV_FP16 = 1 };
 
-/* Bytes of workspace a plan with these bounds needs. */
+/* Bytes of workspace a plan with these bounds needs: total work items over
+ * the batch, and the largest number of work items of one request. */
 int64_t pg_decode_workspace_bytes(int32_t batch_size, int32_t num_qo_heads,
-                                  int64_t max_items);
+                                  int64_t total_items, int64_t max_items_per_request);
 
 /* Split-count selection for 256-CU MI355X: pages per work item such that the
  * whole launch fills the GPU in (close to) whole waves of workgroups.

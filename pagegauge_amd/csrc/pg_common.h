@@ -53,16 +53,27 @@ __device__ __forceinline__ float wave_sum(float v) {
   return v;
 }
 
-// Reductions over the 16 lanes of one DPP row (lanes 16*r .. 16*r+15).
+// Reductions over the 16 lanes of one DPP row (lanes 16*r .. 16*r+15):
+// rotations by 8, 4, 2, 1 within the row leave every lane with the result.
+template <int kRor>
+__device__ __forceinline__ float row_ror(float v) {
+  return __builtin_bit_cast(
+      float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0x120 + kRor, 0xf, 0xf, false));
+}
+
 __device__ __forceinline__ float row16_max(float v) {
-#pragma unroll
-  for (int offset = 8; offset > 0; offset >>= 1) v = fmaxf(v, __shfl_xor(v, offset, kWave));
+  v = fmaxf(v, row_ror<8>(v));
+  v = fmaxf(v, row_ror<4>(v));
+  v = fmaxf(v, row_ror<2>(v));
+  v = fmaxf(v, row_ror<1>(v));
   return v;
 }
 
 __device__ __forceinline__ float row16_sum(float v) {
-#pragma unroll
-  for (int offset = 8; offset > 0; offset >>= 1) v += __shfl_xor(v, offset, kWave);
+  v += row_ror<8>(v);
+  v += row_ror<4>(v);
+  v += row_ror<2>(v);
+  v += row_ror<1>(v);
   return v;
 }
 

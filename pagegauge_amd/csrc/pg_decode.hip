@@ -34,6 +34,7 @@
 #include "pg_common.h"
 
 #include <algorithm>
+#include <cmath>
 #include <vector>
 
 namespace pg {
@@ -44,13 +45,16 @@ typedef _Float16 v8h __attribute__((ext_vector_type(8)));
 typedef _Float16 v4h __attribute__((ext_vector_type(4)));
 typedef _Float16 v2h __attribute__((ext_vector_type(2)));
 typedef float v4f __attribute__((ext_vector_type(4)));
-typedef unsigned char u8x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t v2u __attribute__((ext_vector_type(2)));
+typedef uint32_t v4u __attribute__((ext_vector_type(4)));
 
 constexpr int kGroupPages = 4;          // INT8 pages per PV MFMA (k = 64 tokens)
 constexpr int kMaxWavesPerBlock = 8;
-constexpr int kLdsPerWave = 1024;       // INT8 P digits: [4 pages][4 heads][4 digits][16 tokens]
+constexpr int kLdsPerWave = 1024;       // INT8 P digits: [4 pages][4 heads][4 digit rows][16 tokens]
 constexpr int kCombineThreads = 256;
 constexpr int kMaxItemsPerRequest = 4096;
+constexpr int kMaxChunkPages = 64;      // pages per work item (one wave lane per page)
+constexpr int kMinChunkPages = 4;       // balanced plans keep at least one PV group per item
 constexpr float kNegInf = -__builtin_huge_valf();
 
 struct WorkItem {
@@ -60,8 +64,8 @@ struct WorkItem {
   int32_t page_begin;  // absolute index into the segment's page-index array
   int32_t page_end;    // exclusive
   int32_t last_page;   // absolute index of the segment's final page for the request
-  int32_t pad0;
-  int32_t pad1;
+  int32_t item_in_request;  // position of this item among its request's items
+  int32_t pad;
 };
 static_assert(sizeof(WorkItem) == 32, "work item layout");
 
@@ -85,46 +89,39 @@ struct DecodeArgs {
   int num_qo_heads;
   int num_kv_heads;
   int waves_per_block;
+  int max_items;      // partial rows per (request, head)
   float sm_scale_log2;
 };
 
 // Per-lane softmax/output state of one KV head (4 query heads).
-// Lane l owns head h = l/16; o[nb] is output dim 64*(nb/4) + 4*(l%16) + nb%4.
+// Lane l owns head h = l/16; o[nb] is output dim 8*(l%16) + nb.
 struct HeadState {
   float m;
   float l;
   float o[8];
 };
 
-__device__ __forceinline__ uint32_t bits_of(u8x4 v) { return __builtin_bit_cast(uint32_t, v); }
-__device__ __forceinline__ u8x4 bytes_of(uint32_t v) { return __builtin_bit_cast(u8x4, v); }
-
 // 4x4 byte transpose: r[k] holds 4 dims of token k; returns c[j] holding
-// dim j of tokens 0..3.
+// dim j of tokens 0..3.  v_perm_b32(hi, lo, sel) picks byte sel_i of the
+// 8-byte value {hi:lo} (bytes 0-3 = lo) for result byte i.
 __device__ __forceinline__ void transpose4x4(const uint32_t r[4], uint32_t c[4]) {
-  const u8x4 a = bytes_of(r[0]), b = bytes_of(r[1]), cc = bytes_of(r[2]), d = bytes_of(r[3]);
-  const u8x4 t0 = __builtin_shufflevector(a, b, 0, 4, 1, 5);
-  const u8x4 t1 = __builtin_shufflevector(a, b, 2, 6, 3, 7);
-  const u8x4 t2 = __builtin_shufflevector(cc, d, 0, 4, 1, 5);
-  const u8x4 t3 = __builtin_shufflevector(cc, d, 2, 6, 3, 7);
-  c[0] = bits_of(__builtin_shufflevector(t0, t2, 0, 1, 4, 5));
-  c[1] = bits_of(__builtin_shufflevector(t0, t2, 2, 3, 6, 7));
-  c[2] = bits_of(__builtin_shufflevector(t1, t3, 0, 1, 4, 5));
-  c[3] = bits_of(__builtin_shufflevector(t1, t3, 2, 3, 6, 7));
+  const uint32_t t0 = __builtin_amdgcn_perm(r[1], r[0], 0x05010400u);  // r0.b0 r1.b0 r0.b1 r1.b1
+  const uint32_t t1 = __builtin_amdgcn_perm(r[1], r[0], 0x07030602u);  // r0.b2 r1.b2 r0.b3 r1.b3
+  const uint32_t t2 = __builtin_amdgcn_perm(r[3], r[2], 0x05010400u);
+  const uint32_t t3 = __builtin_amdgcn_perm(r[3], r[2], 0x07030602u);
+  c[0] = __builtin_amdgcn_perm(t2, t0, 0x05040100u);  // r0.b0 r1.b0 r2.b0 r3.b0
+  c[1] = __builtin_amdgcn_perm(t2, t0, 0x07060302u);
+  c[2] = __builtin_amdgcn_perm(t3, t1, 0x05040100u);
+  c[3] = __builtin_amdgcn_perm(t3, t1, 0x07060302u);
 }
 
-// Balanced radix-256 digits of |x| <= 2^22: x = d0*2^16 + d1*2^8 + d2.
-__device__ __forceinline__ void balanced_digits(int x, int& d0, int& d1, int& d2) {
-  d2 = ((x + 128) & 255) - 128;
-  const int r = (x - d2) >> 8;
-  d1 = ((r + 128) & 255) - 128;
-  d0 = (r - d1) >> 8;
-}
-
-__device__ __forceinline__ int select_digit(int x, int which) {
-  int d0, d1, d2;
-  balanced_digits(x, d0, d1, d2);
-  return which == 0 ? d0 : (which == 1 ? d1 : (which == 2 ? d2 : 0));
+// Pins ``x`` in registers at this point: uses after it cannot be hoisted
+// above it, and the wait for its load is placed here (not earlier).
+template <typename T>
+__device__ __forceinline__ void consume_point(T& x) {
+  T value = x;
+  asm volatile("" : "+v"(value));
+  x = value;
 }
 
 // Exponent e with 0 < v < 2^e (v > 0); 0 for v == 0.
@@ -132,11 +129,6 @@ __device__ __forceinline__ int ceil_exponent(float v) {
   int e = 0;
   if (v > 0.0f) frexpf(v, &e);
   return e;
-}
-
-__device__ __forceinline__ float combine_digits(v4i acc) {
-  return static_cast<float>(acc.x) * 65536.0f + static_cast<float>(acc.y) * 256.0f +
-         static_cast<float>(acc.z);
 }
 
 __device__ __forceinline__ void wave_lds_fence() {
@@ -176,11 +168,38 @@ __device__ __forceinline__ int clamp_page_slot(int slot, int begin, int end) {
   return slot < end ? slot : end - 1;
 }
 
+struct Int8Group {
+  v4i k[4][2];      // K codes: [page of the group][bytes 16*kg.. and 64+16*kg..] of token lane%16
+  v2u v[16];        // V codes: 8 dims of page lane/16, tokens 0..15
+};
+
 // ---------------------------------------------------------------------------
 // INT8 page-affine chunk: pages [it.page_begin, it.page_end) of one request,
-// KV head ``kv``.  Groups of 4 pages; loads of group g+1 are issued before
-// group g is computed.
+// KV head ``kv``, in groups of 4 pages.  kRowStride is the byte distance of
+// two token rows (Hkv*128) when known at compile time, else 0.
+//
+// Fixed point: the query of head h is rounded to a 23-bit integer
+// q_int = rint(q * 2^qe) (|q_int| < 2^22) and split into balanced radix-256
+// digits q_int = 65536*d0 + 256*d1 + d2 (|d0| <= 64, |d1|, |d2| <= 128); A rows
+// 4h, 4h+1, 4h+2 hold them, row 4h+3 is zero.  Scores are
+// (65536*C[4h] + 256*C[4h+1] + C[4h+2]) * 2^-qe * sm_scale*log2(e) * sK, an
+// exact integer dot product up to the final float conversion.  Probabilities
+// use the same three digits relative to the chunk's largest V page scale:
+// P_int = rint(p * sV * 2^pe) < 2^22.
 // ---------------------------------------------------------------------------
+__device__ __forceinline__ void three_digits(int x, int& d0, int& d1, int& d2) {
+  d2 = ((x + 128) & 255) - 128;
+  const int r = (x - d2) >> 8;
+  d1 = ((r + 128) & 255) - 128;
+  d0 = (r - d1) >> 8;
+}
+
+__device__ __forceinline__ float from_digits(v4i acc) {
+  return static_cast<float>(acc.x) * 65536.0f + static_cast<float>(acc.y) * 256.0f +
+         static_cast<float>(acc.z);
+}
+
+template <int kRowStride>
 __device__ __forceinline__ void int8_chunk(const DecodeArgs& a, const WorkItem& it, int kv,
                                            int lane, uint8_t* lds, HeadState& st) {
   const int hkv = a.num_kv_heads;
@@ -188,27 +207,70 @@ __device__ __forceinline__ void int8_chunk(const DecodeArgs& a, const WorkItem& 
   const int kg = lane >> 4;
   const int a_head = m16 >> 2;   // A-operand row 4h+c -> head h, digit c
   const int a_digit = m16 & 3;
-  const int64_t row_stride = static_cast<int64_t>(hkv) * kHeadDim;   // one token row (bytes)
+  const int64_t row_stride = kRowStride ? kRowStride : static_cast<int64_t>(hkv) * kHeadDim;
+  const int64_t page_stride = row_stride * kPageSize;
   const int8_t* kc = static_cast<const int8_t*>(a.k_cache) + kv * kHeadDim;
   const int8_t* vc = static_cast<const int8_t*>(a.v_cache) + kv * kHeadDim;
 
-  // ---- query digits (A operand of QK): dims 16*kg + 64*j + b, b = 0..15
+  const int begin = it.page_begin;
+  const int count = it.page_end - it.page_begin;   // 1..64 (planner bound)
+  const int last_slot = it.last_page - begin;      // slot of the segment's final page (may be >= count)
+  const int groups = (count + kGroupPages - 1) / kGroupPages;
+
+  // Chunk metadata, one lane per page slot: physical page and K/V page scales.
+  const int my_page = a.indices[begin + min(lane, count - 1)];
+
+  // ---- query (A operand of QK): dims 16*kg + 64*j + b, b = 0..15
   const uint16_t* q = a.query + it.request * a.query_batch_stride +
                       static_cast<int64_t>(kv * kGqa + a_head) * kHeadDim;
-  float qv[2][16];
-  float qmax = 0.0f;
+  v8h qraw[2][2];
 #pragma unroll
   for (int j = 0; j < 2; ++j) {
-    const uint4 lo = *reinterpret_cast<const uint4*>(q + 16 * kg + 64 * j);
-    const uint4 hi = *reinterpret_cast<const uint4*>(q + 16 * kg + 64 * j + 8);
-    const uint32_t w[8] = {lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w};
-#pragma unroll
-    for (int b = 0; b < 8; ++b) {
-      qv[j][2 * b] = half_bits_to_float(static_cast<uint16_t>(w[b] & 0xffffu));
-      qv[j][2 * b + 1] = half_bits_to_float(static_cast<uint16_t>(w[b] >> 16));
-      qmax = fmaxf(qmax, fmaxf(fabsf(qv[j][2 * b]), fabsf(qv[j][2 * b + 1])));
-    }
+    qraw[j][0] = *reinterpret_cast<const v8h*>(q + 16 * kg + 64 * j);
+    qraw[j][1] = *reinterpret_cast<const v8h*>(q + 16 * kg + 64 * j + 8);
   }
+  const int last_len = it.segment == 0 ? a.last_page_len[it.request] : a.tail_last_len[it.request];
+
+  // page scales (after the index arrives); the V scale's chunk maximum fixes
+  // the probability fixed point for the whole chunk
+  const float my_sk = lane < count ? half_bits_to_float(a.k_scale[static_cast<int64_t>(my_page) * hkv + kv]) : 0.0f;
+  const float my_sv = lane < count ? half_bits_to_float(a.v_scale[static_cast<int64_t>(my_page) * hkv + kv]) : 0.0f;
+
+  // Group buffers, double buffered: K [page][2 x 16 bytes] of token m16;
+  // V: 8 dims (8*m16 ..) of page kg, 16 tokens.  Slots past the chunk end
+  // re-read its last page: their scores are masked to -inf and their
+  // probabilities (hence digits) are zero.
+  Int8Group buf[2];
+  const int64_t k_lane = static_cast<int64_t>(m16) * row_stride + 16 * kg;
+  auto issue = [&](int g, Int8Group& dst) {
+#pragma unroll
+    for (int i = 0; i < kGroupPages; ++i) {
+      const int page = __builtin_amdgcn_readlane(my_page, min(g * kGroupPages + i, count - 1));
+      const int8_t* base = kc + static_cast<int64_t>(page) * page_stride + k_lane;
+      dst.k[i][0] = *reinterpret_cast<const v4i*>(base);
+      dst.k[i][1] = *reinterpret_cast<const v4i*>(base + 64);
+    }
+    int vpage = __builtin_amdgcn_readlane(my_page, min(g * kGroupPages, count - 1));
+#pragma unroll
+    for (int i = 1; i < kGroupPages; ++i) {
+      const int pi = __builtin_amdgcn_readlane(my_page, min(g * kGroupPages + i, count - 1));
+      vpage = kg == i ? pi : vpage;
+    }
+    const int8_t* vbase = vc + static_cast<int64_t>(vpage) * page_stride + 8 * m16;
+#pragma unroll
+    for (int t = 0; t < kPageSize; ++t)
+      dst.v[t] = *reinterpret_cast<const v2u*>(vbase + t * row_stride);
+  };
+  issue(0, buf[0]);
+
+  // ---- query digits (overlaps the first group's loads)
+  float qmax = 0.0f;
+#pragma unroll
+  for (int j = 0; j < 2; ++j)
+#pragma unroll
+    for (int h = 0; h < 2; ++h)
+#pragma unroll
+      for (int b = 0; b < 8; ++b) qmax = fmaxf(qmax, fabsf(static_cast<float>(qraw[j][h][b])));
   // max over the 16 lanes sharing a_head (lane bits 0,1,4,5)
   qmax = fmaxf(qmax, __shfl_xor(qmax, 1, kWave));
   qmax = fmaxf(qmax, __shfl_xor(qmax, 2, kWave));
@@ -218,118 +280,85 @@ __device__ __forceinline__ void int8_chunk(const DecodeArgs& a, const WorkItem& 
   v4i qd[2];
 #pragma unroll
   for (int j = 0; j < 2; ++j) {
-    uint32_t packed[4];
+    int packed[4];
 #pragma unroll
     for (int w = 0; w < 4; ++w) {
       uint32_t word = 0;
 #pragma unroll
       for (int b = 0; b < 4; ++b) {
-        const int qi = static_cast<int>(rintf(ldexpf(qv[j][4 * w + b], q_exp)));
-        const int digit = select_digit(qi, a_digit);
+        const int e = 4 * w + b;
+        const float qf = static_cast<float>(qraw[j][e >> 3][e & 7]);
+        int d0, d1, d2;
+        three_digits(static_cast<int>(rintf(ldexpf(qf, q_exp))), d0, d1, d2);
+        const int digit = a_digit == 0 ? d0 : (a_digit == 1 ? d1 : (a_digit == 2 ? d2 : 0));
         word |= (static_cast<uint32_t>(digit) & 0xffu) << (8 * b);
       }
-      packed[w] = word;
+      packed[w] = static_cast<int>(word);
     }
-    qd[j] = v4i{static_cast<int>(packed[0]), static_cast<int>(packed[1]),
-                static_cast<int>(packed[2]), static_cast<int>(packed[3])};
+    qd[j] = v4i{packed[0], packed[1], packed[2], packed[3]};
   }
   // score scale for this lane's C row (head kg): 2^-q_exp(head kg) * sm_scale*log2e
-  const int q_exp_row = __shfl(q_exp, 4 * kg, kWave);
-  const float qscale = ldexpf(a.sm_scale_log2, -q_exp_row);
+  const float qscale = ldexpf(a.sm_scale_log2, -__shfl(q_exp, 4 * kg, kWave));
+  float vmax = my_sv;
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) vmax = fmaxf(vmax, __shfl_xor(vmax, off, kWave));
+  const int p_exp = 22 - ceil_exponent(vmax);      // p*sV*2^p_exp < 2^22 since p <= 1
+  const float p_unit = ldexpf(1.0f, p_exp);
+  const float inv_p = ldexpf(1.0f, -p_exp);
 
   // zero the wave's digit buffer once: digit row 3 of every head stays zero
   *reinterpret_cast<uint4*>(lds + 16 * lane) = uint4{0u, 0u, 0u, 0u};
   wave_lds_fence();
 
-  const int begin = it.page_begin;
-  const int end = it.page_end;
-  const int last_page = it.last_page;
-  const int last_len = it.segment == 0 ? a.last_page_len[it.request] : a.tail_last_len[it.request];
-  const int32_t* indices = a.indices;
-  const int groups = (end - begin + kGroupPages - 1) / kGroupPages;
-
-  // group buffers
-  v4i kb[kGroupPages][2];
-  uint32_t vb[2][kPageSize];
-  int page_id[kGroupPages];
-
-  auto issue = [&](int g, v4i (&kbuf)[kGroupPages][2], uint32_t (&vbuf)[2][kPageSize],
-                   int (&ids)[kGroupPages]) {
-    // Slots past the chunk end keep a valid page id (for the scale loads) but
-    // load nothing; their scores are masked to -inf.
+  // PV partial sums stay in the MFMA accumulators (exact int32) while the
+  // running max is unchanged; they are folded into st.o when it rises and at
+  // the end.  Per digit row and group the sum is below 64 tokens * 128 * 127
+  // < 2^20, so 16 groups (the 64-page chunk bound) stay below 2^24 (exact in
+  // float as well).
+  v4i pv[8];
 #pragma unroll
-    for (int i = 0; i < kGroupPages; ++i) {
-      const int slot = clamp_page_slot(begin + g * kGroupPages + i, begin, end);
-      ids[i] = indices[slot];
-    }
+  for (int nb = 0; nb < 8; ++nb) pv[nb] = v4i{0, 0, 0, 0};
+  auto fold = [&](float scale) {
 #pragma unroll
-    for (int i = 0; i < kGroupPages; ++i) {
-      if (begin + g * kGroupPages + i < end) {
-        const int8_t* base =
-            kc + (static_cast<int64_t>(ids[i]) * kPageSize + m16) * row_stride + 16 * kg;
-        kbuf[i][0] = *reinterpret_cast<const v4i*>(base);
-        kbuf[i][1] = *reinterpret_cast<const v4i*>(base + 64);
-      } else {
-        kbuf[i][0] = v4i{0, 0, 0, 0};
-        kbuf[i][1] = v4i{0, 0, 0, 0};
-      }
-    }
-    // V: this lane reads page kg of the group, dims 4*m16 (+64), all 16 tokens
-    int my_page = ids[0];
-#pragma unroll
-    for (int i = 1; i < kGroupPages; ++i) my_page = kg == i ? ids[i] : my_page;
-    if (begin + g * kGroupPages + kg < end) {
-      const int8_t* vbase = vc + static_cast<int64_t>(my_page) * kPageSize * row_stride + 4 * m16;
-#pragma unroll
-      for (int t = 0; t < kPageSize; ++t) {
-        vbuf[0][t] = *reinterpret_cast<const uint32_t*>(vbase + t * row_stride);
-        vbuf[1][t] = *reinterpret_cast<const uint32_t*>(vbase + t * row_stride + 64);
-      }
-    } else {
-#pragma unroll
-      for (int t = 0; t < kPageSize; ++t) {
-        vbuf[0][t] = 0u;
-        vbuf[1][t] = 0u;
-      }
+    for (int nb = 0; nb < 8; ++nb) {
+      st.o[nb] = (st.o[nb] + from_digits(pv[nb]) * inv_p) * scale;
+      pv[nb] = v4i{0, 0, 0, 0};
     }
   };
 
-  if (groups > 0) issue(0, kb, vb, page_id);
-  for (int g = 0; g < groups; ++g) {
-    v4i kn[kGroupPages][2];
-    uint32_t vn[2][kPageSize];
-    int next_id[kGroupPages];
-    if (g + 1 < groups) issue(g + 1, kn, vn, next_id);
-
-    // ---- QK: exact integer scores, recombined in float
+  auto compute = [&](int g, Int8Group& cur) {
+#pragma unroll
+    for (int i = 0; i < kGroupPages; ++i) {
+      consume_point(cur.k[i][0]);
+      consume_point(cur.k[i][1]);
+    }
+#pragma unroll
+    for (int t = 0; t < kPageSize; ++t) consume_point(cur.v[t]);
+    // ---- QK: exact integer dot products
     float s[kGroupPages];
     float sv[kGroupPages];
 #pragma unroll
     for (int i = 0; i < kGroupPages; ++i) {
       v4i acc = {0, 0, 0, 0};
-      acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(qd[0], kb[i][0], acc, 0, 0, 0);
-      acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(qd[1], kb[i][1], acc, 0, 0, 0);
-      const int slot = begin + g * kGroupPages + i;
-      const float sk = half_bits_to_float(a.k_scale[static_cast<int64_t>(page_id[i]) * hkv + kv]);
-      bool valid = slot < end;
-      sv[i] = valid ? half_bits_to_float(a.v_scale[static_cast<int64_t>(page_id[i]) * hkv + kv]) : 0.0f;
-      if (slot == last_page && m16 >= last_len) valid = false;
-      s[i] = valid ? combine_digits(acc) * (qscale * sk) : kNegInf;
+      acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(qd[0], cur.k[i][0], acc, 0, 0, 0);
+      acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(qd[1], cur.k[i][1], acc, 0, 0, 0);
+      const int slot = g * kGroupPages + i;
+      const int ls = min(slot, count - 1);
+      const float sk = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, my_sk), ls));
+      sv[i] = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, my_sv), ls));
+      const bool valid = slot < count && !(slot == last_slot && m16 >= last_len);
+      s[i] = valid ? from_digits(acc) * (qscale * sk) : kNegInf;
     }
     float p[kGroupPages];
     const float alpha = softmax_update<kGroupPages>(st, s, p);
+    if (__builtin_amdgcn_ballot_w64(alpha != 1.0f)) fold(alpha);
 
-    // ---- P digits (fixed point relative to the group's largest V scale)
-    float vmax = sv[0];
-#pragma unroll
-    for (int i = 1; i < kGroupPages; ++i) vmax = fmaxf(vmax, sv[i]);
-    const int p_exp = 22 - ceil_exponent(vmax);   // p*sV*2^p_exp < 2^22 since p <= 1
+    // ---- P digits -> LDS [page i][head kg][digit][token m16]
 #pragma unroll
     for (int i = 0; i < kGroupPages; ++i) {
-      const int pi = static_cast<int>(rintf(ldexpf(p[i] * sv[i], p_exp)));
       int d0, d1, d2;
-      balanced_digits(pi, d0, d1, d2);
-      uint8_t* row = lds + ((i * 4 + kg) * 4) * 16 + m16;   // [page i][head kg][digit][token]
+      three_digits(static_cast<int>(rintf(p[i] * sv[i] * p_unit)), d0, d1, d2);
+      uint8_t* row = lds + ((i * 4 + kg) * 4) * 16 + m16;
       row[0] = static_cast<uint8_t>(d0);
       row[16] = static_cast<uint8_t>(d1);
       row[32] = static_cast<uint8_t>(d2);
@@ -339,15 +368,17 @@ __device__ __forceinline__ void int8_chunk(const DecodeArgs& a, const WorkItem& 
     const v4i pa = *reinterpret_cast<const v4i*>(lds + ((kg * 4 + a_head) * 4 + a_digit) * 16);
     wave_lds_fence();
 
-    // ---- PV: V code bytes transposed to token-major operands
-    const float inv_p = ldexpf(1.0f, -p_exp);
+    // ---- PV: V code bytes transposed to token-major operands; n-block nb
+    // covers output dim 8*(lane%16) + nb
 #pragma unroll
     for (int half = 0; half < 2; ++half) {
       uint32_t cols[4][4];   // [dim j][token quad]
 #pragma unroll
       for (int tq = 0; tq < 4; ++tq) {
+        const uint32_t r[4] = {cur.v[4 * tq][half], cur.v[4 * tq + 1][half], cur.v[4 * tq + 2][half],
+                               cur.v[4 * tq + 3][half]};
         uint32_t c[4];
-        transpose4x4(&vb[half][4 * tq], c);
+        transpose4x4(r, c);
 #pragma unroll
         for (int j = 0; j < 4; ++j) cols[j][tq] = c[j];
       }
@@ -355,37 +386,36 @@ __device__ __forceinline__ void int8_chunk(const DecodeArgs& a, const WorkItem& 
       for (int j = 0; j < 4; ++j) {
         const v4i bop = {static_cast<int>(cols[j][0]), static_cast<int>(cols[j][1]),
                          static_cast<int>(cols[j][2]), static_cast<int>(cols[j][3])};
-        v4i acc = {0, 0, 0, 0};
-        acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(pa, bop, acc, 0, 0, 0);
-        const int nb = half * 4 + j;
-        st.o[nb] = st.o[nb] * alpha + combine_digits(acc) * inv_p;
+        pv[4 * half + j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(pa, bop, pv[4 * half + j], 0, 0, 0);
       }
     }
+  };
 
-    if (g + 1 < groups) {
-#pragma unroll
-      for (int i = 0; i < kGroupPages; ++i) {
-        kb[i][0] = kn[i][0];
-        kb[i][1] = kn[i][1];
-        page_id[i] = next_id[i];
-      }
-#pragma unroll
-      for (int t = 0; t < kPageSize; ++t) {
-        vb[0][t] = vn[0][t];
-        vb[1][t] = vn[1][t];
-      }
-    }
+  // Software pipeline: the loads of group g+1 are in flight while group g is
+  // computed; consume_point keeps the compiler from pulling g+1's uses (and
+  // their waits) into iteration g.  The steady-state loop has no branches
+  // around loads; the last one or two groups are peeled.
+  int g = 0;
+  for (; g + 2 < groups; g += 2) {
+    issue(g + 1, buf[1]);
+    compute(g, buf[0]);
+    issue(g + 2, buf[0]);
+    compute(g + 1, buf[1]);
   }
+  if (g + 1 < groups) {
+    issue(g + 1, buf[1]);
+    compute(g, buf[0]);
+    compute(g + 1, buf[1]);
+  } else {
+    compute(g, buf[0]);
+  }
+  fold(1.0f);
 }
 
 // ---------------------------------------------------------------------------
 // FP16 chunk (tail ring or plain FP16 pages), one page per step.
 // ---------------------------------------------------------------------------
-__device__ __forceinline__ v2h pair_of(uint32_t lo_token, uint32_t hi_token, int upper) {
-  const v2h a = __builtin_bit_cast(v2h, lo_token);
-  const v2h b = __builtin_bit_cast(v2h, hi_token);
-  return upper ? __builtin_shufflevector(a, b, 1, 3) : __builtin_shufflevector(a, b, 0, 2);
-}
+__device__ __forceinline__ uint32_t word_of(v4u v, int i) { return v[i]; }
 
 __device__ __forceinline__ void fp16_pages(const DecodeArgs& a, int request, const uint16_t* kpages,
                                            const uint16_t* vpages, const int32_t* indices,
@@ -397,6 +427,9 @@ __device__ __forceinline__ void fp16_pages(const DecodeArgs& a, int request, con
   const int64_t row_stride = static_cast<int64_t>(hkv) * kHeadDim;  // elements
   const uint16_t* kp = kpages + kv * kHeadDim;
   const uint16_t* vp = vpages + kv * kHeadDim;
+  const int count = end - begin;        // 1..64 (planner bound)
+  const int last_slot = last_page - begin;
+  const int my_page = lane < count ? indices[begin + lane] : 0;
 
   // Q operand: head h on row 4h; lanes of other rows hold zeros.
   v8h qa[4];
@@ -411,42 +444,53 @@ __device__ __forceinline__ void fp16_pages(const DecodeArgs& a, int request, con
       qa[j] = v8h{0, 0, 0, 0, 0, 0, 0, 0};
     }
   }
-  uint16_t* plds = reinterpret_cast<uint16_t*>(lds);   // [4 heads][16 tokens] fp16
+  uint16_t* plds = reinterpret_cast<uint16_t*>(lds);   // [4 heads][2 parts][16 tokens] fp16
 
-  v8h kb[4];
-  uint32_t vb[4][2][2];   // [token k][half][dword]
-  auto issue = [&](int slot, v8h (&kbuf)[4], uint32_t (&vbuf)[4][2][2]) {
-    const int page = indices[slot];
+  struct Fp16Page {
+    v8h k[4];    // K row of token lane%16: halves 32*j + 8*kg .. +7
+    v4u v[4];    // V: dims 8*m16 .. +7 of tokens 4*kg + k
+  };
+  Fp16Page buf[2];
+  auto issue = [&](int slot, Fp16Page& dst) {
+    const int page = __builtin_amdgcn_readlane(my_page, slot);
     const uint16_t* kbase = kp + (static_cast<int64_t>(page) * kPageSize + m16) * row_stride + 8 * kg;
 #pragma unroll
-    for (int j = 0; j < 4; ++j) kbuf[j] = *reinterpret_cast<const v8h*>(kbase + 32 * j);
+    for (int j = 0; j < 4; ++j) dst.k[j] = *reinterpret_cast<const v8h*>(kbase + 32 * j);
 #pragma unroll
     for (int k = 0; k < 4; ++k) {
       const uint16_t* vbase =
-          vp + (static_cast<int64_t>(page) * kPageSize + 4 * kg + k) * row_stride + 4 * m16;
-#pragma unroll
-      for (int half = 0; half < 2; ++half) {
-        const uint2 w = *reinterpret_cast<const uint2*>(vbase + 64 * half);
-        vbuf[k][half][0] = w.x;
-        vbuf[k][half][1] = w.y;
-      }
+          vp + (static_cast<int64_t>(page) * kPageSize + 4 * kg + k) * row_stride + 8 * m16;
+      dst.v[k] = *reinterpret_cast<const v4u*>(vbase);
     }
   };
 
-  if (begin < end) issue(begin, kb, vb);
-  for (int slot = begin; slot < end; ++slot) {
-    v8h kn[4];
-    uint32_t vn[4][2][2];
-    if (slot + 1 < end) issue(slot + 1, kn, vn);
+  // PV sums accumulate in the MFMA accumulators (rows 4h: hi part, 4h+1: lo
+  // part) and are folded into st.o when the running max rises and at the end.
+  v4f pv[8];
+#pragma unroll
+  for (int nb = 0; nb < 8; ++nb) pv[nb] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+  auto fold = [&](float scale) {
+#pragma unroll
+    for (int nb = 0; nb < 8; ++nb) {
+      st.o[nb] = (st.o[nb] + pv[nb].x + pv[nb].y) * scale;
+      pv[nb] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+    }
+  };
 
+  auto compute = [&](int slot, Fp16Page& cur) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) consume_point(cur.k[j]);
+#pragma unroll
+    for (int k = 0; k < 4; ++k) consume_point(cur.v[k]);
     v4f acc = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-    for (int j = 0; j < 4; ++j) acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(qa[j], kb[j], acc, 0, 0, 0);
+    for (int j = 0; j < 4; ++j) acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(qa[j], cur.k[j], acc, 0, 0, 0);
     bool valid = true;
-    if (slot == last_page && m16 >= last_len) valid = false;
+    if (slot == last_slot && m16 >= last_len) valid = false;
     float s[1] = {valid ? acc.x * a.sm_scale_log2 : kNegInf};
     float p[1];
     const float alpha = softmax_update<1>(st, s, p);
+    if (__builtin_amdgcn_ballot_w64(alpha != 1.0f)) fold(alpha);
 
     // P as an FP16 hi/lo pair (p = hi + lo to ~22 bits) -> LDS [head][part][token];
     // A operand rows 4h (hi) and 4h+1 (lo) read 4 tokens each, rows 4h+2/3 are 0.
@@ -461,33 +505,34 @@ __device__ __forceinline__ void fp16_pages(const DecodeArgs& a, int request, con
     wave_lds_fence();
 
 #pragma unroll
-    for (int half = 0; half < 2; ++half) {
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const int dw = j >> 1;
-        const int upper = j & 1;
-        const v2h p01 = pair_of(vb[0][half][dw], vb[1][half][dw], upper);
-        const v2h p23 = pair_of(vb[2][half][dw], vb[3][half][dw], upper);
-        const v4h bop = __builtin_shufflevector(p01, p23, 0, 1, 2, 3);
-        v4f o = {0.0f, 0.0f, 0.0f, 0.0f};
-        o = __builtin_amdgcn_mfma_f32_16x16x16f16(pa, bop, o, 0, 0, 0);
-        const int nb = half * 4 + j;
-        st.o[nb] = st.o[nb] * alpha + (o.x + o.y);
-      }
+    for (int nb = 0; nb < 8; ++nb) {
+      const int dw = nb >> 1;
+      const uint32_t sel = (nb & 1) ? 0x07060302u : 0x05040100u;
+      // (token 4kg, token 4kg+1) and (4kg+2, 4kg+3) halves of dim 8*m16+nb
+      const uint32_t p01 = __builtin_amdgcn_perm(word_of(cur.v[1], dw), word_of(cur.v[0], dw), sel);
+      const uint32_t p23 = __builtin_amdgcn_perm(word_of(cur.v[3], dw), word_of(cur.v[2], dw), sel);
+      const v4h bop = __builtin_shufflevector(__builtin_bit_cast(v2h, p01),
+                                              __builtin_bit_cast(v2h, p23), 0, 1, 2, 3);
+      pv[nb] = __builtin_amdgcn_mfma_f32_16x16x16f16(pa, bop, pv[nb], 0, 0, 0);
     }
+  };
 
-    if (slot + 1 < end) {
-#pragma unroll
-      for (int j = 0; j < 4; ++j) kb[j] = kn[j];
-#pragma unroll
-      for (int k = 0; k < 4; ++k)
-#pragma unroll
-        for (int half = 0; half < 2; ++half) {
-          vb[k][half][0] = vn[k][half][0];
-          vb[k][half][1] = vn[k][half][1];
-        }
-    }
+  issue(0, buf[0]);
+  int slot = 0;
+  for (; slot + 2 < count; slot += 2) {
+    issue(slot + 1, buf[1]);
+    compute(slot, buf[0]);
+    issue(slot + 2, buf[0]);
+    compute(slot + 1, buf[1]);
   }
+  if (slot + 1 < count) {
+    issue(slot + 1, buf[1]);
+    compute(slot, buf[0]);
+    compute(slot + 1, buf[1]);
+  } else {
+    compute(slot, buf[0]);
+  }
+  fold(1.0f);
 }
 
 __device__ __forceinline__ void init_state(HeadState& st) {
@@ -507,7 +552,10 @@ __global__ __launch_bounds__(kWave * kMaxWavesPerBlock) void decode_partial_kern
   HeadState st;
   init_state(st);
   if (it.kind == PG_KV_INT8) {
-    int8_chunk(a, it, kv, lane, lds, st);
+    if (a.num_kv_heads == 8)
+      int8_chunk<8 * kHeadDim>(a, it, kv, lane, lds, st);
+    else
+      int8_chunk<0>(a, it, kv, lane, lds, st);
   } else if (it.segment == 0) {
     fp16_pages(a, it.request, static_cast<const uint16_t*>(a.k_cache),
                static_cast<const uint16_t*>(a.v_cache), a.indices, it.page_begin, it.page_end,
@@ -516,14 +564,17 @@ __global__ __launch_bounds__(kWave * kMaxWavesPerBlock) void decode_partial_kern
     fp16_pages(a, it.request, a.tail_k, a.tail_v, a.tail_indices, it.page_begin, it.page_end,
                it.last_page, a.tail_last_len[it.request], kv, lane, lds, st);
   }
-  // partial write: lane (head l/16, n = l%16) owns dims 4n..4n+3 and 64+4n..64+4n+3
+  // partial write: lane (head l/16, n = l%16) owns dims 8n..8n+7.  Layout
+  // [request][qo head][item of the request][128] so a combine block reads one
+  // (request, head) as a contiguous run.
   const float l_row = row16_sum(st.l);
   const int qh = kv * kGqa + (lane >> 4);
   const int n = lane & 15;
-  const int64_t row = static_cast<int64_t>(blockIdx.x) * a.num_qo_heads + qh;
-  float* o = a.partial_o + row * kHeadDim;
-  *reinterpret_cast<float4*>(o + 4 * n) = make_float4(st.o[0], st.o[1], st.o[2], st.o[3]);
-  *reinterpret_cast<float4*>(o + 64 + 4 * n) = make_float4(st.o[4], st.o[5], st.o[6], st.o[7]);
+  const int64_t row = (static_cast<int64_t>(it.request) * a.num_qo_heads + qh) * a.max_items +
+                      it.item_in_request;
+  float* o = a.partial_o + row * kHeadDim + 8 * n;
+  *reinterpret_cast<float4*>(o) = make_float4(st.o[0], st.o[1], st.o[2], st.o[3]);
+  *reinterpret_cast<float4*>(o + 4) = make_float4(st.o[4], st.o[5], st.o[6], st.o[7]);
   if (n == 0) {
     a.partial_m[row] = st.m;
     a.partial_l[row] = l_row;
@@ -531,8 +582,13 @@ __global__ __launch_bounds__(kWave * kMaxWavesPerBlock) void decode_partial_kern
 }
 
 // ---------------------------------------------------------------------------
-// Combine: one block per (request, query head).
+// Combine: block (request*Hq + head, dim quarter); 256 threads = 32 item rows
+// x 8 float4 columns, so one pass loads 32 partials of 32 dims in parallel.
 // ---------------------------------------------------------------------------
+constexpr int kCombineRows = 32;
+constexpr int kCombineCols = 8;      // float4 columns = 32 dims
+constexpr int kCombineInRegs = 8;   // item rows per thread held in registers (256 items)
+
 struct CombineArgs {
   const float* partial_o;
   const float* partial_m;
@@ -543,6 +599,7 @@ struct CombineArgs {
   uint16_t* out;
   float* lse;
   int num_qo_heads;
+  int max_items;
 };
 
 __device__ __forceinline__ float block_reduce(float v, float* scratch, bool is_max) {
@@ -557,64 +614,93 @@ __device__ __forceinline__ float block_reduce(float v, float* scratch, bool is_m
   return r;
 }
 
+__device__ __forceinline__ void fma4(float4& acc, float w, const float4& v) {
+  acc.x += w * v.x;
+  acc.y += w * v.y;
+  acc.z += w * v.z;
+  acc.w += w * v.w;
+}
+
 __global__ __launch_bounds__(kCombineThreads) void combine_kernel(CombineArgs a) {
-  __shared__ float weights[kMaxItemsPerRequest];
   __shared__ float scratch[kCombineThreads / kWave];
-  __shared__ float2 partial_acc[kCombineThreads / kWave][kWave];
-  const int request = blockIdx.x / a.num_qo_heads;
-  const int qh = blockIdx.x % a.num_qo_heads;
-  const int begin = a.item_ptr[request];
-  const int count = a.item_ptr[request + 1] - begin;
+  __shared__ float4 partial_acc[kCombineRows][kCombineCols];
+  __shared__ float partial_l[kCombineThreads / kWave];
+  const int row_head = blockIdx.x;
+  const int request = row_head / a.num_qo_heads;
+  const int qh = row_head % a.num_qo_heads;
+  const int count = a.item_ptr[request + 1] - a.item_ptr[request];
   const int tid = threadIdx.x;
+  const int r = tid / kCombineCols;
+  const int c = tid % kCombineCols;
+  const int dim = 32 * blockIdx.y + 4 * c;
+  const int64_t base = static_cast<int64_t>(row_head) * a.max_items;
+  const float* pm = a.partial_m + base;
+  const float* pl = a.partial_l + base;
+  const float* po = a.partial_o + base * kHeadDim + dim;
 
+  // One round trip: every load of this block is issued before any reduction.
+  float4 ov[kCombineInRegs];
+  float mv[kCombineInRegs], lv[kCombineInRegs];
+#pragma unroll
+  for (int k = 0; k < kCombineInRegs; ++k) {
+    const int j = r + k * kCombineRows;
+    const bool in = j < count;
+    ov[k] = in ? *reinterpret_cast<const float4*>(po + static_cast<int64_t>(j) * kHeadDim)
+               : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    mv[k] = in ? pm[j] : kNegInf;
+    lv[k] = in ? pl[j] : 0.0f;
+  }
   float local_max = kNegInf;
-  for (int i = tid; i < count; i += kCombineThreads)
-    local_max = fmaxf(local_max, a.partial_m[static_cast<int64_t>(begin + i) * a.num_qo_heads + qh]);
+#pragma unroll
+  for (int k = 0; k < kCombineInRegs; ++k) local_max = fmaxf(local_max, mv[k]);
+  for (int j = r + kCombineInRegs * kCombineRows; j < count; j += kCombineRows)
+    local_max = fmaxf(local_max, pm[j]);
   const float m = block_reduce(local_max, scratch, true);
-  float local_sum = 0.0f;
-  for (int i = tid; i < count; i += kCombineThreads) {
-    const int64_t row = static_cast<int64_t>(begin + i) * a.num_qo_heads + qh;
-    const float mi = a.partial_m[row];
-    const float w = (mi == kNegInf) ? 0.0f : exp2f(mi - m);
-    weights[i] = w;
-    local_sum += w * a.partial_l[row];
-  }
-  const float l = block_reduce(local_sum, scratch, false);   // includes a __syncthreads
 
-  const int wave = tid / kWave;
-  const int lane = tid % kWave;
-  float2 acc = make_float2(0.0f, 0.0f);
-  for (int i = wave; i < count; i += kCombineThreads / kWave) {
-    const float w = weights[i];
-    if (w != 0.0f) {
-      const float2 o = *reinterpret_cast<const float2*>(
-          a.partial_o + (static_cast<int64_t>(begin + i) * a.num_qo_heads + qh) * kHeadDim + 2 * lane);
-      acc.x += w * o.x;
-      acc.y += w * o.y;
-    }
+  float4 acc = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+  float lsum = 0.0f;
+#pragma unroll
+  for (int k = 0; k < kCombineInRegs; ++k) {
+    const float w = mv[k] == kNegInf ? 0.0f : exp2f(mv[k] - m);
+    fma4(acc, w, ov[k]);
+    lsum += w * lv[k];
   }
-  partial_acc[wave][lane] = acc;
+  for (int j = r + kCombineInRegs * kCombineRows; j < count; j += kCombineRows) {
+    const float mj = pm[j];
+    const float w = mj == kNegInf ? 0.0f : exp2f(mj - m);
+    fma4(acc, w, *reinterpret_cast<const float4*>(po + static_cast<int64_t>(j) * kHeadDim));
+    lsum += w * pl[j];
+  }
+  // l is summed once per item row (column 0 of each row)
+  lsum = wave_sum(c == 0 ? lsum : 0.0f);
+  partial_acc[r][c] = acc;
+  if (tid % kWave == 0) partial_l[tid / kWave] = lsum;
   __syncthreads();
-  if (wave == 0) {
-    float2 total = partial_acc[0][lane];
-    for (int w = 1; w < kCombineThreads / kWave; ++w) {
-      total.x += partial_acc[w][lane].x;
-      total.y += partial_acc[w][lane].y;
+  if (tid < kCombineCols) {
+    float4 total = partial_acc[0][tid];
+    for (int k = 1; k < kCombineRows; ++k) {
+      const float4 v = partial_acc[k][tid];
+      total.x += v.x;
+      total.y += v.y;
+      total.z += v.z;
+      total.w += v.w;
     }
+    float l = 0.0f;
+    for (int w = 0; w < kCombineThreads / kWave; ++w) l += partial_l[w];
     const bool empty = !(l > 0.0f);
-    float ox = empty ? 0.0f : total.x / l;
-    float oy = empty ? 0.0f : total.y / l;
+    const float inv = empty ? 0.0f : 1.0f / l;
+    float o4[4] = {total.x * inv, total.y * inv, total.z * inv, total.w * inv};
+    const int d = 32 * blockIdx.y + 4 * tid;
     if (a.value_center != nullptr) {
-      const int kv = qh / kGqa;
-      const uint16_t* c = a.value_center + request * a.center_batch_stride + kv * kHeadDim + 2 * lane;
-      ox += half_bits_to_float(c[0]);
-      oy += half_bits_to_float(c[1]);
+      const uint16_t* cv = a.value_center + request * a.center_batch_stride + (qh / kGqa) * kHeadDim + d;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) o4[e] += half_bits_to_float(cv[e]);
     }
-    const __half2 h = __floats2half2_rn(ox, oy);
-    *reinterpret_cast<__half2*>(a.out + (static_cast<int64_t>(request) * a.num_qo_heads + qh) * kHeadDim +
-                                2 * lane) = h;
-    if (lane == 0 && a.lse != nullptr)
-      a.lse[static_cast<int64_t>(request) * a.num_qo_heads + qh] = empty ? kNegInf : log2f(l) + m;
+    uint16_t* out = a.out + static_cast<int64_t>(row_head) * kHeadDim + d;
+    *reinterpret_cast<__half2*>(out) = __floats2half2_rn(o4[0], o4[1]);
+    *reinterpret_cast<__half2*>(out + 2) = __floats2half2_rn(o4[2], o4[3]);
+    if (tid == 0 && blockIdx.y == 0 && a.lse != nullptr)
+      a.lse[row_head] = empty ? kNegInf : log2f(l) + m;
   }
 }
 
@@ -684,7 +770,7 @@ __global__ __launch_bounds__(kWave * kMaxWavesPerBlock) void tail_merge_kernel(T
   const uint16_t* c = t.value_center + request * t.center_batch_stride + kv * kHeadDim;
 #pragma unroll
   for (int nb = 0; nb < 8; ++nb) {
-    const int d = 64 * (nb >> 2) + 4 * n + (nb & 3);
+    const int d = 8 * n + nb;
     const float merged = (w_old * half_bits_to_float(o[d]) + w_new * st.o[nb]) * inv +
                          half_bits_to_float(c[d]);
     o[d] = __half_as_ushort(__float2half_rn(merged));
@@ -706,31 +792,31 @@ int64_t align_up(int64_t v, int64_t a) { return (v + a - 1) / a * a; }
 using namespace pg;
 
 extern "C" int64_t pg_decode_workspace_bytes(int32_t batch_size, int32_t num_qo_heads,
-                                             int64_t max_items) {
-  if (batch_size <= 0 || num_qo_heads <= 0 || max_items <= 0) return 0;
-  int64_t bytes = align_up(max_items * static_cast<int64_t>(sizeof(WorkItem)), 256);
+                                             int64_t total_items, int64_t max_items_per_request) {
+  if (batch_size <= 0 || num_qo_heads <= 0 || total_items <= 0 || max_items_per_request <= 0)
+    return 0;
+  int64_t bytes = align_up(total_items * static_cast<int64_t>(sizeof(WorkItem)), 256);
   bytes += align_up((batch_size + 1) * static_cast<int64_t>(sizeof(int32_t)), 256);
-  bytes += align_up(max_items * num_qo_heads * static_cast<int64_t>(kHeadDim + 2) * 4, 256);
+  bytes += align_up(static_cast<int64_t>(batch_size) * num_qo_heads * max_items_per_request *
+                        (kHeadDim + 2) * 4, 256);
   return bytes;
 }
 
 extern "C" int32_t pg_select_split_pages(int64_t total_pages, int32_t batch_size,
                                          int32_t num_kv_heads, int32_t bytes_per_page,
                                          int32_t num_cus) {
-  // One workgroup carries all KV heads of a page range, so the number of
-  // workgroups is the number of page chunks.  A 512-thread block of eight
-  // KV-head waves occupies two waves per SIMD, i.e. one block per CU at a
-  // time: aim for one chunk per CU so the whole decode is a single wave of
-  // workgroups.  Chunks never shrink below 4 pages (one PV MFMA group).
-  // ``total_pages`` is weighted in units of ``bytes_per_page``.
+  // Pages per work item when the batch is spread over one workgroup per CU
+  // (a 512-thread block of eight KV-head waves holds a CU at two waves per
+  // SIMD), capped at one wave lane per page.  ``total_pages`` is in units of
+  // ``bytes_per_page``; pg_decode_plan applies the same rule per segment with
+  // nearly equal chunks.
   (void)num_kv_heads;
   (void)bytes_per_page;
-  if (total_pages <= 0) return kGroupPages;
+  if (total_pages <= 0) return 1;
   if (num_cus <= 0) num_cus = 256;
   const int64_t target_items = std::max<int64_t>(num_cus, batch_size);
-  int64_t split = (total_pages + target_items - 1) / target_items;
-  split = std::max<int64_t>(split, kGroupPages);
-  return static_cast<int32_t>(std::min<int64_t>(split, 1 << 20));
+  const int64_t split = (total_pages + target_items - 1) / target_items;
+  return static_cast<int32_t>(std::min<int64_t>(std::max<int64_t>(split, 1), kMaxChunkPages));
 }
 
 extern "C" int32_t pg_decode_plan(const int32_t* host_indptr, const int32_t* host_last_page_len,
@@ -770,39 +856,96 @@ extern "C" int32_t pg_decode_plan(const int32_t* host_indptr, const int32_t* hos
       tail_pages += tn;
     }
   }
-  const int primary_bytes = primary_kind == PG_KV_INT8 ? 4096 : 8192;
-  if (split_pages <= 0) {
-    // FP16 tail pages cost twice the bytes of INT8 pages
-    const int64_t weighted = primary_pages + (primary_kind == PG_KV_INT8 ? 2 : 1) * tail_pages;
-    split_pages = pg_select_split_pages(weighted, batch_size, num_kv_heads, primary_bytes, num_cus);
+  // Segments of the batch; FP16 pages stream twice the bytes of INT8 pages.
+  struct Segment {
+    int request, kind, seg, begin, end;
+    double weight;
+  };
+  std::vector<Segment> segments;
+  for (int b = 0; b < batch_size; ++b) {
+    if (host_tail_indptr && host_tail_indptr[b + 1] > host_tail_indptr[b])
+      segments.push_back({b, PG_KV_FP16, 1, host_tail_indptr[b], host_tail_indptr[b + 1],
+                          primary_kind == PG_KV_INT8 ? 2.0 : 1.0});
+    if (host_indptr[b + 1] > host_indptr[b])
+      segments.push_back({b, primary_kind, 0, host_indptr[b], host_indptr[b + 1], 1.0});
   }
-  if (tail_split_pages <= 0) {
-    // an FP16 page streams twice the bytes of an INT8 page
-    tail_split_pages = primary_kind == PG_KV_INT8 ? std::max(1, (split_pages + 1) / 2) : split_pages;
+  std::vector<int> chunks(segments.size(), 0);
+  if (split_pages > 0) {
+    // fixed split (FlashInfer fixed_split_size semantics): pages per work item
+    if (tail_split_pages <= 0)
+      tail_split_pages = primary_kind == PG_KV_INT8 ? std::max(1, (split_pages + 1) / 2) : split_pages;
+    for (size_t i = 0; i < segments.size(); ++i) {
+      const int n = segments[i].end - segments[i].begin;
+      const int size = std::min(segments[i].seg == 0 ? split_pages : tail_split_pages, kMaxChunkPages);
+      chunks[i] = (n + size - 1) / size;
+    }
+  } else {
+    // Balanced plan: the smallest per-item load ``cap`` (weighted pages) for
+    // which the whole batch fits in one workgroup per CU; every segment is
+    // cut into nearly equal chunks of at most kMaxChunkPages pages.
+    const int64_t target = std::max<int64_t>(num_cus > 0 ? num_cus : 256, 1);
+    const int64_t min_chunk = kMinChunkPages;
+    auto count_for = [&](double cap, std::vector<int>* out) {
+      int64_t total = 0;
+      for (size_t i = 0; i < segments.size(); ++i) {
+        const int n = segments[i].end - segments[i].begin;
+        const int64_t by_cap = static_cast<int64_t>(std::ceil(n * segments[i].weight / cap - 1e-9));
+        const int64_t by_size = (n + kMaxChunkPages - 1) / kMaxChunkPages;
+        const int64_t most = std::max<int64_t>(1, n / min_chunk);
+        const int64_t c = std::max<int64_t>({1, by_size, std::min(by_cap, most)});
+        if (out) (*out)[i] = static_cast<int>(c);
+        total += c;
+      }
+      return total;
+    };
+    double lo = 1e-3, hi = 1.0;
+    for (const Segment& sg : segments) hi += (sg.end - sg.begin) * sg.weight;
+    // Measured on MI355X (B1/49K split sweep): once the batch has a few
+    // thousand pages, 16-page chunks beat finer ones because each work
+    // item pays a fixed start-up (page-table load, then the first group);
+    // smaller problems use chunks down to one PV group for parallelism.
+    lo = hi >= 12.0 * static_cast<double>(target) ? 16.0 : 1e-3;
+    if (count_for(hi, nullptr) <= target) {
+      for (int iter = 0; iter < 64; ++iter) {
+        const double mid = 0.5 * (lo + hi);
+        if (count_for(mid, nullptr) <= target) hi = mid; else lo = mid;
+      }
+    }
+    count_for(hi, &chunks);
   }
 
   std::vector<WorkItem> items;
   std::vector<int32_t> item_ptr(batch_size + 1, 0);
   int max_per_request = 0;
+  split_pages = 0;
+  tail_split_pages = 0;
+  size_t next = 0;
   for (int b = 0; b < batch_size; ++b) {
-    // Tail (FP16) items of a request come first so they start in the first
-    // wave of workgroups next to the INT8 chunks instead of trailing them.
+    // A request's items are contiguous; its FP16 tail items come first so
+    // they start in the first wave of workgroups beside the INT8 chunks.
     item_ptr[b] = static_cast<int32_t>(items.size());
-    if (host_tail_indptr) {
-      const int tb = host_tail_indptr[b], te = host_tail_indptr[b + 1];
-      for (int s = tb; s < te; s += tail_split_pages)
-        items.push_back(WorkItem{b, PG_KV_FP16, 1, s, std::min(te, s + tail_split_pages), te - 1, 0, 0});
+    for (; next < segments.size() && segments[next].request == b; ++next) {
+      const Segment& sg = segments[next];
+      const int n = sg.end - sg.begin;
+      const int c = chunks[next];
+      int start = sg.begin;
+      for (int k = 0; k < c; ++k) {
+        const int size = n / c + (k < n % c ? 1 : 0);
+        items.push_back(WorkItem{b, sg.kind, sg.seg, start, start + size, sg.end - 1,
+                                 static_cast<int32_t>(items.size()) - item_ptr[b], 0});
+        start += size;
+        if (sg.seg == 0) split_pages = std::max(split_pages, size);
+        else tail_split_pages = std::max(tail_split_pages, size);
+      }
     }
-    const int pb = host_indptr[b], pe = host_indptr[b + 1];
-    for (int s = pb; s < pe; s += split_pages)
-      items.push_back(WorkItem{b, primary_kind, 0, s, std::min(pe, s + split_pages), pe - 1, 0, 0});
     max_per_request = std::max(max_per_request, static_cast<int>(items.size()) - item_ptr[b]);
   }
   item_ptr[batch_size] = static_cast<int32_t>(items.size());
   if (max_per_request > kMaxItemsPerRequest)
     return fail(PG_ERROR_UNSUPPORTED, "too many splits per request; raise split_pages");
   const int64_t n_items = std::max<int64_t>(1, static_cast<int64_t>(items.size()));
-  const int64_t needed = pg_decode_workspace_bytes(batch_size, num_qo_heads, n_items);
+  const int64_t needed =
+      pg_decode_workspace_bytes(batch_size, num_qo_heads, n_items, std::max(1, max_per_request));
   if (needed > workspace_bytes)
     return fail(PG_ERROR_WORKSPACE, "decode workspace too small: need " + std::to_string(needed) +
                                         " bytes, have " + std::to_string(workspace_bytes));
@@ -851,11 +994,12 @@ struct PartialViews {
 
 PartialViews partial_views(const pg_decode_plan_t* plan, void* workspace) {
   uint8_t* ws = static_cast<uint8_t*>(workspace);
-  const int64_t n_items = std::max<int64_t>(1, plan->num_items);
+  const int64_t rows = static_cast<int64_t>(plan->batch_size) * plan->num_qo_heads *
+                      std::max(1, plan->max_items_per_request);
   PartialViews v;
   v.o = reinterpret_cast<float*>(ws + plan->partial_offset);
-  v.m = v.o + n_items * plan->num_qo_heads * kHeadDim;
-  v.l = v.m + n_items * plan->num_qo_heads;
+  v.m = v.o + rows * kHeadDim;
+  v.l = v.m + rows;
   return v;
 }
 
@@ -904,6 +1048,7 @@ extern "C" int32_t pg_decode_run_partial(const pg_decode_plan_t* plan, const voi
   a.num_qo_heads = plan->num_qo_heads;
   a.num_kv_heads = plan->num_kv_heads;
   a.waves_per_block = waves_per_block_for(plan->num_kv_heads);
+  a.max_items = std::max(1, plan->max_items_per_request);
   a.sm_scale_log2 = sm_scale * 1.4426950408889634f;
   const dim3 grid(plan->num_items, plan->num_kv_heads / a.waves_per_block);
   hipLaunchKernelGGL(decode_partial_kernel, grid, dim3(kWave * a.waves_per_block), 0,
@@ -928,7 +1073,8 @@ extern "C" int32_t pg_decode_run_combine(const pg_decode_plan_t* plan, const voi
   c.out = static_cast<uint16_t*>(out);
   c.lse = lse;
   c.num_qo_heads = plan->num_qo_heads;
-  hipLaunchKernelGGL(combine_kernel, dim3(plan->batch_size * plan->num_qo_heads),
+  c.max_items = std::max(1, plan->max_items_per_request);
+  hipLaunchKernelGGL(combine_kernel, dim3(plan->batch_size * plan->num_qo_heads, kHeadDim / 32),
                      dim3(kCombineThreads), 0, as_stream(stream), c);
   return check_launch("decode_combine");
 }
