@@ -180,8 +180,13 @@ int32_t pg_select_split_pages(int64_t total_pages, int32_t batch_size, int32_t n
 
 /* Plan a decode.  host_indptr [B+1] / host_last_page_len [B]: segment 0
  * (INT8 codes or FP16 pages, primary_kind); host_tail_indptr/_last_len: the
- * optional FP16 tail segment (NULL if none).  split_pages / tail_split_pages
- * <= 0 select automatically (pg_select_split_pages).  Writes the work list
+ * optional FP16 tail segment (NULL if none).  split_pages > 0 cuts each
+ * request's segment 0 of n pages into ceil(n / split_pages) nearly equal
+ * items (the item count of FlashInfer's fixed_split_size, balanced sizes);
+ * the tail likewise with tail_split_pages, default ceil(split_pages/2) for
+ * INT8 (an FP16 page streams twice the bytes);
+ * split_pages <= 0 balances the batch over num_cus workgroups (every item at
+ * most 64 pages, FP16 pages weighted twice INT8 pages).  Writes the work list
  * into the device workspace (synchronous copy on ``stream``).  Replaces
  * BatchDecodeWithPagedKVCacheWrapper.plan as called by
  * scripts/benchmark_flashinfer_page_affine_int8.py:363-389. */
@@ -192,6 +197,22 @@ int32_t pg_decode_plan(const int32_t* host_indptr, const int32_t* host_last_page
                        int32_t page_size, int32_t split_pages, int32_t tail_split_pages,
                        int32_t num_cus, void* workspace, int64_t workspace_bytes,
                        pg_decode_plan_t* plan, void* stream);
+
+/* The host half of pg_decode_plan (same arguments, same validation and
+ * errors) without a device: fills *plan and, if items_out != NULL, the work
+ * list as 8 int32 per item {request, kind (PG_KV_*), segment (0 primary,
+ * 1 tail), page_begin, page_end (positions in indices/tail_indices), last
+ * position of the segment, item index inside its request, 0}; item_ptr_out
+ * (if != NULL) receives [B+1] offsets of each request's items.  Call once
+ * with items_out NULL to learn plan->num_items.  For inspection and tests of
+ * the scheduler; no reference counterpart (FlashInfer's plan info is opaque). */
+int32_t pg_decode_plan_host(const int32_t* host_indptr, const int32_t* host_last_page_len,
+                            int32_t batch_size, int32_t primary_kind,
+                            const int32_t* host_tail_indptr, const int32_t* host_tail_last_len,
+                            int32_t num_qo_heads, int32_t num_kv_heads, int32_t head_dim,
+                            int32_t page_size, int32_t split_pages, int32_t tail_split_pages,
+                            int32_t num_cus, pg_decode_plan_t* plan, int32_t* items_out,
+                            int64_t items_capacity, int32_t* item_ptr_out);
 
 /* Run a planned decode.  Segment 0: pages ``indices`` (indptr/last_page_len
  * as planned; last_page_len is re-read on the device every call, so a

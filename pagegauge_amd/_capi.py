@@ -67,6 +67,8 @@ PROTOTYPES = {
     "pg_select_split_pages": (_i32, [_i64, _i32, _i32, _i32, _i32]),
     "pg_decode_plan": (_i32, [_p, _p, _i32, _i32, _p, _p, _i32, _i32, _i32, _i32, _i32, _i32,
                               _i32, _p, _i64, ctypes.POINTER(DecodePlan), _p]),
+    "pg_decode_plan_host": (_i32, [_p, _p, _i32, _i32, _p, _p, _i32, _i32, _i32, _i32, _i32,
+                                   _i32, _i32, ctypes.POINTER(DecodePlan), _p, _i64, _p]),
     "pg_decode_run": (_i32, [ctypes.POINTER(DecodePlan), _p, _i64, _p, _p, _p, _p, _p, _p, _p, _p,
                              _p, _p, _p, _i64, _p, _p, _f32, _p, _p]),
     "pg_decode_run_partial": (_i32, [ctypes.POINTER(DecodePlan), _p, _i64, _p, _p, _p, _p, _p, _p,

@@ -35,6 +35,7 @@
 
 #include <algorithm>
 #include <cmath>
+#include <cstring>
 #include <vector>
 
 namespace pg {
@@ -819,16 +820,17 @@ extern "C" int32_t pg_select_split_pages(int64_t total_pages, int32_t batch_size
   return static_cast<int32_t>(std::min<int64_t>(std::max<int64_t>(split, 1), kMaxChunkPages));
 }
 
-extern "C" int32_t pg_decode_plan(const int32_t* host_indptr, const int32_t* host_last_page_len,
-                                  int32_t batch_size, int32_t primary_kind,
-                                  const int32_t* host_tail_indptr,
-                                  const int32_t* host_tail_last_len, int32_t num_qo_heads,
-                                  int32_t num_kv_heads, int32_t head_dim, int32_t page_size,
-                                  int32_t split_pages, int32_t tail_split_pages, int32_t num_cus,
-                                  void* workspace, int64_t workspace_bytes, pg_decode_plan_t* plan,
-                                  void* stream) {
-  clear_error();
-  if (!host_indptr || !host_last_page_len || !plan || !workspace)
+namespace {
+
+// Host half of the planner: validates the batch and cuts it into work items.
+// Fills ``p`` except for the workspace size check, which the caller does.
+int32_t build_plan(const int32_t* host_indptr, const int32_t* host_last_page_len,
+                   int32_t batch_size, int32_t primary_kind, const int32_t* host_tail_indptr,
+                   const int32_t* host_tail_last_len, int32_t num_qo_heads, int32_t num_kv_heads,
+                   int32_t head_dim, int32_t page_size, int32_t split_pages,
+                   int32_t tail_split_pages, int32_t num_cus, std::vector<WorkItem>& items,
+                   std::vector<int32_t>& item_ptr, pg_decode_plan_t& p) {
+  if (!host_indptr || !host_last_page_len)
     return fail(PG_ERROR_INVALID_ARGUMENT, "null plan argument");
   if (batch_size <= 0) return fail(PG_ERROR_INVALID_ARGUMENT, "batch size must be positive");
   if (head_dim != kHeadDim) return fail(PG_ERROR_UNSUPPORTED, "head dimension must be 128");
@@ -914,8 +916,8 @@ extern "C" int32_t pg_decode_plan(const int32_t* host_indptr, const int32_t* hos
     count_for(hi, &chunks);
   }
 
-  std::vector<WorkItem> items;
-  std::vector<int32_t> item_ptr(batch_size + 1, 0);
+  items.clear();
+  item_ptr.assign(batch_size + 1, 0);
   int max_per_request = 0;
   split_pages = 0;
   tail_split_pages = 0;
@@ -946,11 +948,8 @@ extern "C" int32_t pg_decode_plan(const int32_t* host_indptr, const int32_t* hos
   const int64_t n_items = std::max<int64_t>(1, static_cast<int64_t>(items.size()));
   const int64_t needed =
       pg_decode_workspace_bytes(batch_size, num_qo_heads, n_items, std::max(1, max_per_request));
-  if (needed > workspace_bytes)
-    return fail(PG_ERROR_WORKSPACE, "decode workspace too small: need " + std::to_string(needed) +
-                                        " bytes, have " + std::to_string(workspace_bytes));
 
-  pg_decode_plan_t p{};
+  p = pg_decode_plan_t{};
   p.batch_size = batch_size;
   p.num_qo_heads = num_qo_heads;
   p.num_kv_heads = num_kv_heads;
@@ -968,6 +967,33 @@ extern "C" int32_t pg_decode_plan(const int32_t* host_indptr, const int32_t* hos
   p.item_ptr_offset = align_up(n_items * static_cast<int64_t>(sizeof(WorkItem)), 256);
   p.partial_offset = p.item_ptr_offset + align_up((batch_size + 1) * 4, 256);
   p.workspace_bytes = needed;
+  return PG_OK;
+}
+
+}  // namespace
+
+extern "C" int32_t pg_decode_plan(const int32_t* host_indptr, const int32_t* host_last_page_len,
+                                  int32_t batch_size, int32_t primary_kind,
+                                  const int32_t* host_tail_indptr,
+                                  const int32_t* host_tail_last_len, int32_t num_qo_heads,
+                                  int32_t num_kv_heads, int32_t head_dim, int32_t page_size,
+                                  int32_t split_pages, int32_t tail_split_pages, int32_t num_cus,
+                                  void* workspace, int64_t workspace_bytes, pg_decode_plan_t* plan,
+                                  void* stream) {
+  clear_error();
+  if (!plan || !workspace) return fail(PG_ERROR_INVALID_ARGUMENT, "null plan argument");
+  std::vector<WorkItem> items;
+  std::vector<int32_t> item_ptr;
+  pg_decode_plan_t p{};
+  const int32_t rc = build_plan(host_indptr, host_last_page_len, batch_size, primary_kind,
+                                host_tail_indptr, host_tail_last_len, num_qo_heads, num_kv_heads,
+                                head_dim, page_size, split_pages, tail_split_pages, num_cus, items,
+                                item_ptr, p);
+  if (rc != PG_OK) return rc;
+  if (p.workspace_bytes > workspace_bytes)
+    return fail(PG_ERROR_WORKSPACE, "decode workspace too small: need " +
+                                        std::to_string(p.workspace_bytes) + " bytes, have " +
+                                        std::to_string(workspace_bytes));
 
   hipStream_t s = as_stream(stream);
   uint8_t* ws = static_cast<uint8_t*>(workspace);
@@ -981,6 +1007,36 @@ extern "C" int32_t pg_decode_plan(const int32_t* host_indptr, const int32_t* hos
     return fail(PG_ERROR_LAUNCH, "plan copy failed");
   if (hipStreamSynchronize(s) != hipSuccess) return fail(PG_ERROR_LAUNCH, "plan copy sync failed");
   *plan = p;
+  return PG_OK;
+}
+
+extern "C" int32_t pg_decode_plan_host(const int32_t* host_indptr,
+                                       const int32_t* host_last_page_len, int32_t batch_size,
+                                       int32_t primary_kind, const int32_t* host_tail_indptr,
+                                       const int32_t* host_tail_last_len, int32_t num_qo_heads,
+                                       int32_t num_kv_heads, int32_t head_dim, int32_t page_size,
+                                       int32_t split_pages, int32_t tail_split_pages,
+                                       int32_t num_cus, pg_decode_plan_t* plan,
+                                       int32_t* items_out, int64_t items_capacity,
+                                       int32_t* item_ptr_out) {
+  clear_error();
+  if (!plan) return fail(PG_ERROR_INVALID_ARGUMENT, "null plan argument");
+  std::vector<WorkItem> items;
+  std::vector<int32_t> item_ptr;
+  pg_decode_plan_t p{};
+  const int32_t rc = build_plan(host_indptr, host_last_page_len, batch_size, primary_kind,
+                                host_tail_indptr, host_tail_last_len, num_qo_heads, num_kv_heads,
+                                head_dim, page_size, split_pages, tail_split_pages, num_cus, items,
+                                item_ptr, p);
+  if (rc != PG_OK) return rc;
+  *plan = p;
+  if (items_out) {
+    if (items_capacity < static_cast<int64_t>(items.size()))
+      return fail(PG_ERROR_INVALID_ARGUMENT, "work-item buffer too small: need " +
+                                                 std::to_string(items.size()) + " items");
+    std::memcpy(items_out, items.data(), items.size() * sizeof(WorkItem));
+  }
+  if (item_ptr_out) std::memcpy(item_ptr_out, item_ptr.data(), item_ptr.size() * sizeof(int32_t));
   return PG_OK;
 }
 

@@ -114,6 +114,42 @@ class _Planned:
         return int(self.plan.num_items)
 
 
+WORK_ITEM_FIELDS = ("request", "kind", "segment", "page_begin", "page_end", "last_page",
+                    "item_in_request", "pad")
+
+
+def plan_work_items(indptr, last_page_len, tail_indptr=None, tail_last_page_len=None,
+                    kv_data_type=torch.int8, num_qo_heads: int = HQ, num_kv_heads: int = HKV,
+                    head_dim: int = DIM, page_size: int = PAGE, split_pages: int = 0,
+                    tail_split_pages: int = 0, num_cus: int = 256):
+    """Run the decode scheduler on the host only (no device, no workspace).
+
+    Returns ``(plan, items, item_ptr)``: the ``DecodePlan`` that
+    ``pg_decode_plan`` would produce, the work list as an int32 tensor
+    [num_items, 8] with columns ``WORK_ITEM_FIELDS``, and [B+1] per-request
+    item offsets.  Same validation and error messages as ``plan``.
+    """
+    lib = _capi.library()
+    host_indptr = _host_i32(indptr)
+    host_last = _host_i32(last_page_len)
+    host_tail = None if tail_indptr is None else _host_i32(tail_indptr)
+    host_tail_last = None if tail_last_page_len is None else _host_i32(tail_last_page_len)
+    batch = host_indptr.numel() - 1
+    kind = _capi.PG_KV_INT8 if kv_data_type == torch.int8 else _capi.PG_KV_FP16
+    plan = _capi.DecodePlan()
+    args = (host_indptr.data_ptr(), host_last.data_ptr(), batch, kind,
+            None if host_tail is None else host_tail.data_ptr(),
+            None if host_tail_last is None else host_tail_last.data_ptr(), num_qo_heads,
+            num_kv_heads, head_dim, page_size, int(split_pages), int(tail_split_pages),
+            int(num_cus), ctypes.byref(plan))
+    _capi.check(lib.pg_decode_plan_host(*args, None, 0, None), "decode plan")
+    items = torch.empty(max(1, plan.num_items), len(WORK_ITEM_FIELDS), dtype=torch.int32)
+    item_ptr = torch.empty(batch + 1, dtype=torch.int32)
+    _capi.check(lib.pg_decode_plan_host(*args, items.data_ptr(), items.size(0),
+                                        item_ptr.data_ptr()), "decode plan")
+    return plan, items[:plan.num_items], item_ptr
+
+
 class BoundDecode:
     """A planned decode with every pointer resolved: ``partial()``,
     ``combine()`` and ``__call__`` (both) issue the launches with no tensor

@@ -1,0 +1,98 @@
+"""Invariants of the split scheduler (``pg_decode_plan``), checked on the host
+through ``pg_decode_plan_host``: every page of every segment is covered by
+exactly one work item, items respect the one-lane-per-page cap, a request's
+items are contiguous with their FP16 tail first, and the plan fits the
+256-CU launch it was balanced for."""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from pagegauge_amd import workloads
+from pagegauge_amd.decode import plan_work_items
+
+MAX_CHUNK = 64
+
+
+def _indptr(counts):
+    return np.concatenate([[0], np.cumsum(counts)]).astype(np.int32).tolist()
+
+
+def _check_cover(items, item_ptr, old_counts, tail_counts):
+    batch = len(old_counts)
+    items = items.numpy()
+    assert (items[:, 4] > items[:, 3]).all(), "empty work item"
+    assert (items[:, 4] - items[:, 3] <= MAX_CHUNK).all()
+    old_ptr, tail_ptr = _indptr(old_counts), _indptr(tail_counts)
+    for b in range(batch):
+        mine = items[item_ptr[b]:item_ptr[b + 1]]
+        assert (mine[:, 0] == b).all()
+        assert list(mine[:, 6]) == list(range(len(mine)))          # item_in_request
+        for seg, ptr in ((0, old_ptr), (1, tail_ptr)):
+            rows = mine[mine[:, 2] == seg]
+            covered = sorted(p for r in rows for p in range(r[3], r[4]))
+            assert covered == list(range(ptr[b], ptr[b + 1])), (b, seg)
+            if len(rows):
+                assert (rows[:, 5] == ptr[b + 1] - 1).all()          # last page of the segment
+        if tail_counts[b] and old_counts[b]:
+            segs = list(mine[:, 2])
+            assert segs == sorted(segs, reverse=True), "tail items come first"
+
+
+@pytest.mark.parametrize("old,tail", [([3056], [16]), ([240], [16]), ([1], [1]), ([0], [3]),
+                                      ([7, 0, 300], [16, 2, 0])])
+def test_balanced_plan_covers_every_page_once(old, tail):
+    plan, items, ptr = plan_work_items(_indptr(old), [16] * len(old), _indptr(tail),
+                                       [16] * len(tail))
+    assert plan.num_items == items.shape[0] == ptr[-1]
+    assert plan.num_items <= 256 or plan.num_items == sum(
+        -(-n // MAX_CHUNK) for n in old + tail)
+    _check_cover(items, ptr.tolist(), old, tail)
+    assert plan.max_items_per_request == max(int(ptr[b + 1] - ptr[b]) for b in range(len(old)))
+
+
+def test_b1_49k_plan_uses_sixteen_page_chunks_within_one_wave():
+    plan, items, _ = plan_work_items([0, 3056], [16], [0, 16], [16])
+    sizes = (items[:, 4] - items[:, 3]).numpy()
+    assert plan.num_items <= 256
+    old_sizes = sizes[items[:, 2].numpy() == 0]
+    assert old_sizes.max() - old_sizes.min() <= 1                  # nearly equal chunks
+    assert old_sizes.min() >= 16
+
+
+@pytest.mark.parametrize("seed", workloads.VALIDATION_SEEDS[:3])
+def test_b8_ragged_plan_is_balanced(seed):
+    lengths = workloads.ragged_lengths(seed)
+    old = [(n - 256) // 16 for n in lengths]
+    plan, items, ptr = plan_work_items(_indptr(old), [16] * 8, _indptr([16] * 8), [16] * 8)
+    _check_cover(items, ptr.tolist(), old, [16] * 8)
+    assert plan.num_items <= 256
+    sizes = (items[:, 4] - items[:, 3]).numpy().astype(float)
+    weight = np.where(items[:, 2].numpy() == 1, 2.0, 1.0)               # FP16 pages weigh 2x
+    load = sizes * weight
+    assert load.max() <= 1.25 * np.sort(load)[-len(load) // 4:].mean()
+
+
+def test_fixed_split_follows_fixed_split_size():
+    plan, items, ptr = plan_work_items([0, 100, 130], [16, 5], [0, 16, 20], [16, 16],
+                                       split_pages=32)
+    _check_cover(items, ptr.tolist(), [100, 30], [16, 4])
+    sizes = (items[:, 4] - items[:, 3]).numpy()
+    seg = items[:, 2].numpy()
+    # ceil(n / split) nearly equal items per segment; tail split defaults to ceil(32/2)
+    assert list(sizes[seg == 0]) == [25, 25, 25, 25, 30]
+    assert list(sizes[seg == 1]) == [16, 4]
+    assert plan.split_pages == 30 and plan.tail_split_pages == 16
+
+
+def test_fp16_primary_plan_has_no_tail_weighting():
+    plan, items, ptr = plan_work_items([0, 512], [16], kv_data_type=torch.float16)
+    assert plan.primary_kind == 1 and plan.has_tail == 0
+    _check_cover(items, ptr.tolist(), [512], [0])
+
+
+def test_plan_rejects_too_many_items_per_request():
+    with pytest.raises(RuntimeError, match="too many splits"):
+        plan_work_items([0, 5000], [16], split_pages=1)
