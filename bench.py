@@ -14,8 +14,11 @@ cold sample is preceded by an untimed scrub.  The reference scrubs with a
 256 MiB read-modify-write; on MI355X that leaves the 256 MB Infinity Cache
 full of dirty lines whose write-back then lands inside the timed call, so the
 primary cold state uses a read-only 1 GiB scrub (clean eviction) and the
-reference scrub is reported beside it.  Hot samples run back to back.  HIP events on the launch stream bracket the
-partial kernel (the roofline's dominant kernel) and the whole call.
+reference scrub is reported beside it.  Hot samples run back to back.  HIP
+events on the launch stream bracket the whole call; the partial kernel (the
+roofline's dominant kernel) is timed in separate samples by events that its
+own dispatch stamps (hipExtLaunchKernelGGL), the interval a kernel trace
+reports.
 
 Also reported: the same-way FP16 paged-decode kernel on an FP16 copy of the
 same cache, and the CPU baseline (the C oracle's dense decode of the same
@@ -53,6 +56,11 @@ def parse_args() -> argparse.Namespace:
     p.add_argument("--no-cpu", action="store_true")
     p.add_argument("--no-fp16", action="store_true")
     p.add_argument("--sweep", default="", help="comma list of split sizes to time (pilot sweep)")
+    p.add_argument("--modes", default="cold_clean,cold_rmw,hot",
+                   help="cache states to time (cold_clean is required: it gives value/roofline)")
+    p.add_argument("--pmc-calls", type=int, default=0,
+                   help="counter-collection driver for rocprofv3 --pmc: N cold decode calls, "
+                        "then N plain 64 MiB copies of known size; prints one JSON line, no timing")
     return p.parse_args()
 
 
@@ -69,24 +77,46 @@ def summarize(values_ms):
     }
 
 
-def timed_calls(torch, bound, n, scrub=None):
-    """Per-call HIP events: (partial kernel ms list, whole call ms list).
-
+def call_samples(torch, bound, n, scrub=None):
+    """Whole-call durations (ms): events recorded on the launch stream before
+    the partial kernel and after the combine kernel, plain launches.
     ``scrub`` runs before every sample, outside the events; it also keeps the
-    GPU busy while the host queues the timed launches.
-    """
-    ev = [[torch.cuda.Event(enable_timing=True) for _ in range(3)] for _ in range(n)]
+    GPU busy while the host queues the timed launches."""
+    ev = [[torch.cuda.Event(enable_timing=True) for _ in range(2)] for _ in range(n)]
     for i in range(n):
         if scrub is not None:
             scrub()
         ev[i][0].record()
         bound.partial()
-        ev[i][1].record()
         bound.combine()
-        ev[i][2].record()
+        ev[i][1].record()
     torch.cuda.synchronize()
-    kernel = [a.elapsed_time(b) for a, b, _ in ev]
-    call = [a.elapsed_time(c) for a, _, c in ev]
+    return [a.elapsed_time(b) for a, b in ev]
+
+
+def kernel_samples(torch, bound, n, scrub=None):
+    """Partial-kernel durations (ms) from two events that the kernel's
+    dispatch stamps itself (hipExtLaunchKernelGGL begin/end timestamps: the
+    interval a kernel trace reports, without the launch gap).  Taken in
+    separate samples because stamping the dispatch delays the call."""
+    ev = [[torch.cuda.Event(enable_timing=True) for _ in range(2)] for _ in range(n)]
+    for row in ev:                     # a torch event has a handle once recorded
+        for e in row:
+            e.record()
+    torch.cuda.synchronize()
+    for i in range(n):
+        if scrub is not None:
+            scrub()
+        bound.partial_timed(ev[i][0].cuda_event, ev[i][1].cuda_event)
+        bound.combine()
+    torch.cuda.synchronize()
+    return [a.elapsed_time(b) for a, b in ev]
+
+
+def timed_calls(torch, bound, n, scrub=None):
+    """(partial kernel ms list, whole call ms list), n samples of each."""
+    call = call_samples(torch, bound, n, scrub)
+    kernel = kernel_samples(torch, bound, n, scrub)
     return kernel, call
 
 
@@ -95,13 +125,19 @@ def measure(torch, bound, args, scrub_clean, scrub_rmw):
     line of the cache and no dirty line), cold-rmw (the reference's 256 MiB
     add_ scrub, which also leaves up to 256 MB of dirty lines whose
     write-back lands inside the timed call) and hot (back to back)."""
+    modes = set(args.modes.split(","))
     for _ in range(args.warmup):
         scrub_clean()
         bound()
     torch.cuda.synchronize()
     cold_k, cold_c = timed_calls(torch, bound, args.steps, scrub=scrub_clean)
-    rmw_n = max(10, args.steps // 2)
-    rmw_k, rmw_c = timed_calls(torch, bound, rmw_n, scrub=scrub_rmw)
+    result = {"cold_clean_1gib": {"kernel": summarize(cold_k), "call": summarize(cold_c)},
+              "_cold_kernel_ms": cold_k, "_cold_call_ms": cold_c}
+    if "cold_rmw" in modes:
+        rmw_k, rmw_c = timed_calls(torch, bound, max(10, args.steps // 2), scrub=scrub_rmw)
+        result["cold_rmw_256mib"] = {"kernel": summarize(rmw_k), "call": summarize(rmw_c)}
+    if "hot" not in modes:
+        return result
     # hot: back-to-back calls (no events in between) after a long head-start
     # kernel; per-call time = span / repeats
     hot = []
@@ -116,13 +152,37 @@ def measure(torch, bound, args, scrub_clean, scrub_rmw):
         end.record()
         torch.cuda.synchronize()
         hot.append(start.elapsed_time(end) / args.hot_repeats)
-    return {
-        "cold_clean_1gib": {"kernel": summarize(cold_k), "call": summarize(cold_c)},
-        "cold_rmw_256mib": {"kernel": summarize(rmw_k), "call": summarize(rmw_c)},
-        "hot": {"call": summarize(hot), "repeats_per_sample": args.hot_repeats},
-        "_cold_kernel_ms": cold_k,
-        "_cold_call_ms": cold_c,
-    }
+    result["hot"] = {"call": summarize(hot), "repeats_per_sample": args.hot_repeats}
+    return result
+
+
+def pmc_driver(torch, bound, calls, scrub_clean, device):
+    """Workload for one ``rocprofv3 --pmc`` pass (no timing): ``calls`` cold
+    decode calls, then ``calls`` plain copies of 64 MiB (64 MiB read + 64 MiB
+    written, the known-size reference that calibrates FETCH_SIZE/WRITE_SIZE)."""
+    src = torch.ones(64 << 18, dtype=torch.int32, device=device)
+    dst = torch.empty_like(src)
+    for _ in range(calls):
+        scrub_clean()
+        bound()
+    for _ in range(calls):
+        scrub_clean()
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    return {"pmc_calls": calls, "copy_bytes": src.numel() * 4}
+
+
+def committed_traffic(root: Path):
+    """HBM bytes per launch of the partial kernel from the committed counter
+    summary (two rocprofv3 --pmc passes, FETCH_SIZE and WRITE_SIZE, scaled by
+    the plain-copy calibration), or None."""
+    path = root / "profiles" / "decode_partial_b1_49k_pmc.md"
+    if not path.exists():
+        return None
+    for line in path.read_text().splitlines():
+        if line.startswith("traffic_bytes_per_launch:"):
+            return int(line.split(":", 1)[1].strip())
+    return None
 
 
 def cpu_baseline(w, budget_s: float):
@@ -184,6 +244,10 @@ def main() -> int:
     scrub_clean_buf = torch.ones(args.big_scrub_mib * (1 << 20) // 4, dtype=torch.int32, device=device)
     scrub_sink = torch.empty((), dtype=torch.int32, device=device)
     scrub_clean = lambda: torch.amax(scrub_clean_buf, dim=0, out=scrub_sink)  # noqa: E731
+
+    if args.pmc_calls:
+        print(json.dumps(pmc_driver(torch, bound, args.pmc_calls, scrub_clean, device)), flush=True)
+        return 0
 
     # contract timed region: K cold steps bracketed by synchronize
     torch.cuda.synchronize()
@@ -276,7 +340,9 @@ def main() -> int:
             "peak": HBM_PEAK_GBPS,
             "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBPS, 4),
-            "traffic": None,
+            "traffic": committed_traffic(ROOT),
+            "traffic_source": "profiles/decode_partial_b1_49k_pmc.md (FETCH_SIZE + WRITE_SIZE, "
+                              "calibrated by a plain copy)",
             "algorithmic_bytes": alg_bytes,
             "kernel_mean_us": round(kernel_mean_us, 3),
         },
@@ -285,7 +351,7 @@ def main() -> int:
         "timings_fp16_same_way": None if fp16 is None else {k: v for k, v in fp16.items() if not k.startswith("_")},
         "speedup_vs_fp16_same_way": None if fp16 is None else {
             mode: round(fp16[mode]["call"]["p50_us"] / int8[mode]["call"]["p50_us"], 4)
-            for mode in ("cold_clean_1gib", "cold_rmw_256mib", "hot")},
+            for mode in ("cold_clean_1gib", "cold_rmw_256mib", "hot") if mode in int8},
         "parity_vs_oracle": parity,
         "split_sweep": sweep or None,
         "wall_s_timed_region": round(wall_s, 3),

@@ -251,6 +251,20 @@ int32_t pg_decode_run_partial(const pg_decode_plan_t* plan, const void* query,
                               const void* tail_k, const void* tail_v, const int32_t* tail_indices,
                               const int32_t* tail_last_len, float sm_scale, void* workspace,
                               void* stream);
+/* pg_decode_run_partial with kernel timing: start_event / stop_event
+ * (hipEvent_t created with timing enabled, either may be NULL) receive the
+ * partial kernel's own dispatch begin/end timestamps (hipExtLaunchKernelGGL),
+ * so hipEventElapsedTime gives the kernel duration without the launch gap
+ * that events recorded around the call include.  For benchmarks; no
+ * reference counterpart. */
+int32_t pg_decode_run_partial_timed(const pg_decode_plan_t* plan, const void* query,
+                                    int64_t query_batch_stride, const void* k_cache,
+                                    const void* v_cache, const void* k_scale, const void* v_scale,
+                                    const int32_t* indices, const int32_t* last_page_len,
+                                    const void* tail_k, const void* tail_v,
+                                    const int32_t* tail_indices, const int32_t* tail_last_len,
+                                    float sm_scale, void* workspace, void* stream,
+                                    void* start_event, void* stop_event);
 int32_t pg_decode_run_combine(const pg_decode_plan_t* plan, const void* value_center,
                               int64_t center_batch_stride, void* out, float* lse,
                               void* workspace, void* stream);

@@ -33,6 +33,8 @@
 //    merge, divides, adds the value center and writes out/lse.
 #include "pg_common.h"
 
+#include <hip/hip_ext.h>
+
 #include <algorithm>
 #include <cmath>
 #include <cstring>
@@ -1061,14 +1063,14 @@ PartialViews partial_views(const pg_decode_plan_t* plan, void* workspace) {
 
 }  // namespace
 
-extern "C" int32_t pg_decode_run_partial(const pg_decode_plan_t* plan, const void* query,
-                                         int64_t query_batch_stride, const void* k_cache,
-                                         const void* v_cache, const void* k_scale,
-                                         const void* v_scale, const int32_t* indices,
-                                         const int32_t* last_page_len, const void* tail_k,
-                                         const void* tail_v, const int32_t* tail_indices,
-                                         const int32_t* tail_last_len, float sm_scale,
-                                         void* workspace, void* stream) {
+namespace {
+
+int32_t launch_partial(const pg_decode_plan_t* plan, const void* query,
+                       int64_t query_batch_stride, const void* k_cache, const void* v_cache,
+                       const void* k_scale, const void* v_scale, const int32_t* indices,
+                       const int32_t* last_page_len, const void* tail_k, const void* tail_v,
+                       const int32_t* tail_indices, const int32_t* tail_last_len, float sm_scale,
+                       void* workspace, void* stream, void* start_event, void* stop_event) {
   clear_error();
   if (!plan || !query || !workspace) return fail(PG_ERROR_INVALID_ARGUMENT, "null run argument");
   if (plan->num_items_primary > 0) {
@@ -1107,9 +1109,42 @@ extern "C" int32_t pg_decode_run_partial(const pg_decode_plan_t* plan, const voi
   a.max_items = std::max(1, plan->max_items_per_request);
   a.sm_scale_log2 = sm_scale * 1.4426950408889634f;
   const dim3 grid(plan->num_items, plan->num_kv_heads / a.waves_per_block);
-  hipLaunchKernelGGL(decode_partial_kernel, grid, dim3(kWave * a.waves_per_block), 0,
-                     as_stream(stream), a);
+  if (start_event || stop_event) {
+    // The events take the dispatch's own begin/end timestamps.
+    hipExtLaunchKernelGGL(decode_partial_kernel, grid, dim3(kWave * a.waves_per_block), 0,
+                          as_stream(stream), static_cast<hipEvent_t>(start_event),
+                          static_cast<hipEvent_t>(stop_event), 0, a);
+  } else {
+    hipLaunchKernelGGL(decode_partial_kernel, grid, dim3(kWave * a.waves_per_block), 0,
+                       as_stream(stream), a);
+  }
   return check_launch("decode_partial");
+}
+
+}  // namespace
+
+extern "C" int32_t pg_decode_run_partial(const pg_decode_plan_t* plan, const void* query,
+                                         int64_t query_batch_stride, const void* k_cache,
+                                         const void* v_cache, const void* k_scale,
+                                         const void* v_scale, const int32_t* indices,
+                                         const int32_t* last_page_len, const void* tail_k,
+                                         const void* tail_v, const int32_t* tail_indices,
+                                         const int32_t* tail_last_len, float sm_scale,
+                                         void* workspace, void* stream) {
+  return launch_partial(plan, query, query_batch_stride, k_cache, v_cache, k_scale, v_scale,
+                        indices, last_page_len, tail_k, tail_v, tail_indices, tail_last_len,
+                        sm_scale, workspace, stream, nullptr, nullptr);
+}
+
+extern "C" int32_t pg_decode_run_partial_timed(
+    const pg_decode_plan_t* plan, const void* query, int64_t query_batch_stride,
+    const void* k_cache, const void* v_cache, const void* k_scale, const void* v_scale,
+    const int32_t* indices, const int32_t* last_page_len, const void* tail_k, const void* tail_v,
+    const int32_t* tail_indices, const int32_t* tail_last_len, float sm_scale, void* workspace,
+    void* stream, void* start_event, void* stop_event) {
+  return launch_partial(plan, query, query_batch_stride, k_cache, v_cache, k_scale, v_scale,
+                        indices, last_page_len, tail_k, tail_v, tail_indices, tail_last_len,
+                        sm_scale, workspace, stream, start_event, stop_event);
 }
 
 extern "C" int32_t pg_decode_run_combine(const pg_decode_plan_t* plan, const void* value_center,

@@ -163,12 +163,22 @@ class BoundDecode:
         self._state = state
         self._plan_ref = ctypes.byref(state.plan)
         self._partial = lib.pg_decode_run_partial
+        self._partial_timed = lib.pg_decode_run_partial_timed
         self._combine = lib.pg_decode_run_combine
         self._partial_args = (self._plan_ref, *partial_args, state.workspace.data_ptr(), stream)
         self._combine_args = (self._plan_ref, *combine_args, state.workspace.data_ptr(), stream)
 
     def partial(self) -> None:
         rc = self._partial(*self._partial_args)
+        if rc:
+            _capi.check(rc, "decode partial")
+
+    def partial_timed(self, start_event: int, stop_event: int) -> None:
+        """``partial()`` whose kernel dispatch itself stamps two timing events
+        (raw hipEvent_t handles, e.g. ``torch.cuda.Event(enable_timing=True)``
+        ``.cuda_event`` after one ``record()``): their elapsed time is the
+        kernel's duration without the launch gap."""
+        rc = self._partial_timed(*self._partial_args, start_event, stop_event)
         if rc:
             _capi.check(rc, "decode partial")
 
