@@ -58,6 +58,10 @@ constexpr int kCombineThreads = 256;
 constexpr int kMaxItemsPerRequest = 4096;
 constexpr int kMaxChunkPages = 64;      // pages per work item (one wave lane per page)
 constexpr int kMinChunkPages = 4;       // balanced plans keep at least one PV group per item
+#ifndef PG_LARGE_BATCH_MIN_CHUNK
+#define PG_LARGE_BATCH_MIN_CHUNK 16.0
+#endif
+constexpr double kLargeBatchMinChunk = PG_LARGE_BATCH_MIN_CHUNK;  // weighted pages
 constexpr float kNegInf = -__builtin_huge_valf();
 
 struct WorkItem {
@@ -140,41 +144,52 @@ __device__ __forceinline__ void wave_lds_fence() {
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 }
 
-// Online-softmax update for one lane holding ``count`` scores of head row
-// lane/16.  Returns alpha (rescale of the previous state) and writes p[].
+__device__ __forceinline__ int clamp_page_slot(int slot, int begin, int end) {
+  return slot < end ? slot : end - 1;
+}
+
+struct Int8Group {
+  v4i k[4][2];      // K codes of page i: bytes 16*kg.. and 64+16*kg.. of token lane%16
+  v2u v[16];        // V codes [page i][t]: dims 8*(lane%16).. of token 4*(lane/16)+t
+};
+
+// Balanced radix-256 digits of |x| < 2^22 in one step: with
+// y = (x + 0x808080) ^ 0x808080, bytes 0, 1, 2 of y are the int8 digits
+// d2, d1, d0 of x = 65536*d0 + 256*d1 + d2 (each in [-128, 127]).
+__device__ __forceinline__ uint32_t digit_bytes(int x) {
+  return static_cast<uint32_t>(x + 0x808080) ^ 0x808080u;
+}
+
+// Exact-integer recombination of the three digit rows of an accumulator:
+// 65536*acc.x + 256*acc.y + acc.z with |acc.y| < 2^21, |acc.z| < 2^21.
+__device__ __forceinline__ float from_digits(v4i acc) {
+  const int low = (acc.y << 8) + acc.z;
+  return static_cast<float>(acc.x) * 65536.0f + static_cast<float>(low);
+}
+
+// Online-softmax update for chunks whose first step has a visible token (so
+// the running max is finite from then on and no -inf - -inf arises): masked
+// scores are -inf and give p = 0, the first step's alpha is exp2(-inf) = 0.
+// exp2 is the hardware v_exp_f32; results below 2^-126 flush to zero, which
+// is negligible against the row maximum's 1.
 template <int kCount>
-__device__ __forceinline__ float softmax_update(HeadState& st, const float s[kCount],
-                                                float p[kCount]) {
+__device__ __forceinline__ float softmax_update_fast(HeadState& st, const float s[kCount],
+                                                     float p[kCount]) {
   float local = s[0];
 #pragma unroll
   for (int i = 1; i < kCount; ++i) local = fmaxf(local, s[i]);
-  const float group_max = row16_max(local);
-  const float m_new = fmaxf(st.m, group_max);
-  if (m_new == kNegInf) {  // nothing visible yet in this row
-#pragma unroll
-    for (int i = 0; i < kCount; ++i) p[i] = 0.0f;
-    return 1.0f;
-  }
-  const float alpha = exp2f(st.m - m_new);  // exp2(-inf) = 0 on the first visible group
+  const float m_new = fmaxf(st.m, row16_max(local));
+  const float alpha = __builtin_amdgcn_exp2f(st.m - m_new);
   float sum = 0.0f;
 #pragma unroll
   for (int i = 0; i < kCount; ++i) {
-    p[i] = exp2f(s[i] - m_new);
+    p[i] = __builtin_amdgcn_exp2f(s[i] - m_new);
     sum += p[i];
   }
   st.l = st.l * alpha + sum;
   st.m = m_new;
   return alpha;
 }
-
-__device__ __forceinline__ int clamp_page_slot(int slot, int begin, int end) {
-  return slot < end ? slot : end - 1;
-}
-
-struct Int8Group {
-  v4i k[4][2];      // K codes: [page of the group][bytes 16*kg.. and 64+16*kg..] of token lane%16
-  v2u v[16];        // V codes: 8 dims of page lane/16, tokens 0..15
-};
 
 // ---------------------------------------------------------------------------
 // INT8 page-affine chunk: pages [it.page_begin, it.page_end) of one request,
@@ -183,25 +198,18 @@ struct Int8Group {
 //
 // Fixed point: the query of head h is rounded to a 23-bit integer
 // q_int = rint(q * 2^qe) (|q_int| < 2^22) and split into balanced radix-256
-// digits q_int = 65536*d0 + 256*d1 + d2 (|d0| <= 64, |d1|, |d2| <= 128); A rows
-// 4h, 4h+1, 4h+2 hold them, row 4h+3 is zero.  Scores are
+// digits q_int = 65536*d0 + 256*d1 + d2; A rows 4h, 4h+1, 4h+2 of the QK MFMA
+// hold them, row 4h+3 is zero.  Scores are
 // (65536*C[4h] + 256*C[4h+1] + C[4h+2]) * 2^-qe * sm_scale*log2(e) * sK, an
 // exact integer dot product up to the final float conversion.  Probabilities
 // use the same three digits relative to the chunk's largest V page scale:
 // P_int = rint(p * sV * 2^pe) < 2^22.
+//
+// PV contraction order: k-block j (lanes 16j..16j+15 of the B operand) holds
+// tokens 4j..4j+3 of the group's 4 pages, k = 16j + 4t + i for token 4j+t of
+// page i.  Each V load therefore reads one page (a uniform base address) and
+// the P digits of one lane's four pages pack into one dword per digit.
 // ---------------------------------------------------------------------------
-__device__ __forceinline__ void three_digits(int x, int& d0, int& d1, int& d2) {
-  d2 = ((x + 128) & 255) - 128;
-  const int r = (x - d2) >> 8;
-  d1 = ((r + 128) & 255) - 128;
-  d0 = (r - d1) >> 8;
-}
-
-__device__ __forceinline__ float from_digits(v4i acc) {
-  return static_cast<float>(acc.x) * 65536.0f + static_cast<float>(acc.y) * 256.0f +
-         static_cast<float>(acc.z);
-}
-
 template <int kRowStride>
 __device__ __forceinline__ void int8_chunk(const DecodeArgs& a, const WorkItem& it, int kv,
                                            int lane, uint8_t* lds, HeadState& st) {
@@ -221,7 +229,12 @@ __device__ __forceinline__ void int8_chunk(const DecodeArgs& a, const WorkItem& 
   const int groups = (count + kGroupPages - 1) / kGroupPages;
 
   // Chunk metadata, one lane per page slot: physical page and K/V page scales.
+#ifdef PG_PROBE_SAME_PAGE
+  // Timing builds only: every slot reads the chunk's first page (cache-resident).
+  const int my_page = a.indices[begin];
+#else
   const int my_page = a.indices[begin + min(lane, count - 1)];
+#endif
 
   // ---- query (A operand of QK): dims 16*kg + 64*j + b, b = 0..15
   const uint16_t* q = a.query + it.request * a.query_batch_stride +
@@ -239,30 +252,44 @@ __device__ __forceinline__ void int8_chunk(const DecodeArgs& a, const WorkItem& 
   const float my_sk = lane < count ? half_bits_to_float(a.k_scale[static_cast<int64_t>(my_page) * hkv + kv]) : 0.0f;
   const float my_sv = lane < count ? half_bits_to_float(a.v_scale[static_cast<int64_t>(my_page) * hkv + kv]) : 0.0f;
 
-  // Group buffers, double buffered: K [page][2 x 16 bytes] of token m16;
-  // V: 8 dims (8*m16 ..) of page kg, 16 tokens.  Slots past the chunk end
-  // re-read its last page: their scores are masked to -inf and their
-  // probabilities (hence digits) are zero.
+  // Loads: a uniform page base plus a fixed 32-bit lane offset.  Slots past
+  // the chunk end re-read its last page: their scores are masked to -inf and
+  // their probabilities (hence digits) are zero.
   Int8Group buf[2];
-  const int64_t k_lane = static_cast<int64_t>(m16) * row_stride + 16 * kg;
+  const uint32_t k_off = static_cast<uint32_t>(m16 * row_stride + 16 * kg);
+  const uint32_t v_off = static_cast<uint32_t>(4 * kg * row_stride + 8 * m16);
   auto issue = [&](int g, Int8Group& dst) {
+    const int8_t* kp[kGroupPages];
+    const int8_t* vp[kGroupPages];
 #pragma unroll
     for (int i = 0; i < kGroupPages; ++i) {
       const int page = __builtin_amdgcn_readlane(my_page, min(g * kGroupPages + i, count - 1));
-      const int8_t* base = kc + static_cast<int64_t>(page) * page_stride + k_lane;
-      dst.k[i][0] = *reinterpret_cast<const v4i*>(base);
-      dst.k[i][1] = *reinterpret_cast<const v4i*>(base + 64);
+      kp[i] = kc + static_cast<int64_t>(page) * page_stride;
+      vp[i] = vc + static_cast<int64_t>(page) * page_stride;
     }
-    int vpage = __builtin_amdgcn_readlane(my_page, min(g * kGroupPages, count - 1));
+#ifdef PG_PROBE_NO_LOADS
+    // Timing builds only: synthetic operands, no K/V memory traffic.
 #pragma unroll
-    for (int i = 1; i < kGroupPages; ++i) {
-      const int pi = __builtin_amdgcn_readlane(my_page, min(g * kGroupPages + i, count - 1));
-      vpage = kg == i ? pi : vpage;
+    for (int i = 0; i < kGroupPages; ++i) {
+      const int page = static_cast<int>(reinterpret_cast<uintptr_t>(kp[i]) >> 14);
+      dst.k[i][0] = v4i{page ^ lane, page + lane, page * 3, lane * 5};
+      dst.k[i][1] = v4i{page ^ (lane << 3), page - lane, page * 7, lane * 9};
+#pragma unroll
+      for (int t = 0; t < 4; ++t)
+        dst.v[4 * i + t] = v2u{static_cast<uint32_t>(page * 31 + t + lane), static_cast<uint32_t>(page ^ (t << 4) ^ lane)};
     }
-    const int8_t* vbase = vc + static_cast<int64_t>(vpage) * page_stride + 8 * m16;
+#else
 #pragma unroll
-    for (int t = 0; t < kPageSize; ++t)
-      dst.v[t] = *reinterpret_cast<const v2u*>(vbase + t * row_stride);
+    for (int i = 0; i < kGroupPages; ++i) {
+      dst.k[i][0] = *reinterpret_cast<const v4i*>(kp[i] + k_off);
+      dst.k[i][1] = *reinterpret_cast<const v4i*>(kp[i] + k_off + 64);
+    }
+#pragma unroll
+    for (int i = 0; i < kGroupPages; ++i)
+#pragma unroll
+      for (int t = 0; t < 4; ++t)
+        dst.v[4 * i + t] = *reinterpret_cast<const v2u*>(vp[i] + v_off + t * row_stride);
+#endif
   };
   issue(0, buf[0]);
 
@@ -280,23 +307,27 @@ __device__ __forceinline__ void int8_chunk(const DecodeArgs& a, const WorkItem& 
   qmax = fmaxf(qmax, __shfl_xor(qmax, 16, kWave));
   qmax = fmaxf(qmax, __shfl_xor(qmax, 32, kWave));
   const int q_exp = 22 - ceil_exponent(qmax);   // |q| * 2^q_exp < 2^22
+  // this lane's digit is byte 2 - a_digit of the digit bytes (row 3 is zero);
+  // the selector packs it from two words into bytes 0, 1 (0x0c selects zero)
+  const uint32_t q_byte = a_digit == 3 ? 0u : static_cast<uint32_t>(2 - a_digit);
+  const uint32_t q_sel = q_byte | ((q_byte + 4u) << 8) | 0x0c0c0000u;
   v4i qd[2];
 #pragma unroll
   for (int j = 0; j < 2; ++j) {
     int packed[4];
 #pragma unroll
     for (int w = 0; w < 4; ++w) {
-      uint32_t word = 0;
+      uint32_t y[4];
 #pragma unroll
       for (int b = 0; b < 4; ++b) {
         const int e = 4 * w + b;
         const float qf = static_cast<float>(qraw[j][e >> 3][e & 7]);
-        int d0, d1, d2;
-        three_digits(static_cast<int>(rintf(ldexpf(qf, q_exp))), d0, d1, d2);
-        const int digit = a_digit == 0 ? d0 : (a_digit == 1 ? d1 : (a_digit == 2 ? d2 : 0));
-        word |= (static_cast<uint32_t>(digit) & 0xffu) << (8 * b);
+        y[b] = digit_bytes(static_cast<int>(rintf(ldexpf(qf, q_exp))));
       }
-      packed[w] = static_cast<int>(word);
+      // byte b of the word = the selected digit byte of y[b]
+      const uint32_t lo = __builtin_amdgcn_perm(y[1], y[0], q_sel);
+      const uint32_t hi = __builtin_amdgcn_perm(y[3], y[2], q_sel);
+      packed[w] = a_digit == 3 ? 0 : static_cast<int>(lo | (hi << 16));
     }
     qd[j] = v4i{packed[0], packed[1], packed[2], packed[3]};
   }
@@ -306,12 +337,16 @@ __device__ __forceinline__ void int8_chunk(const DecodeArgs& a, const WorkItem& 
 #pragma unroll
   for (int off = 32; off > 0; off >>= 1) vmax = fmaxf(vmax, __shfl_xor(vmax, off, kWave));
   const int p_exp = 22 - ceil_exponent(vmax);      // p*sV*2^p_exp < 2^22 since p <= 1
-  const float p_unit = ldexpf(1.0f, p_exp);
   const float inv_p = ldexpf(1.0f, -p_exp);
+  const float my_svu = ldexpf(my_sv, p_exp);       // sV * 2^p_exp of this lane's page slot
 
   // zero the wave's digit buffer once: digit row 3 of every head stays zero
   *reinterpret_cast<uint4*>(lds + 16 * lane) = uint4{0u, 0u, 0u, 0u};
   wave_lds_fence();
+  // P digit writes: lane (head kg, token m16) -> rows 4*kg + c of k-block m16/4,
+  // bytes 4*(m16%4) .. +3 (pages 0..3)
+  uint32_t* p_dst = reinterpret_cast<uint32_t*>(lds + ((m16 >> 2) * 16 + 4 * kg) * 16 + 4 * (m16 & 3));
+  const v4i* p_src = reinterpret_cast<const v4i*>(lds + (kg * 16 + m16) * 16);
 
   // PV partial sums stay in the MFMA accumulators (exact int32) while the
   // running max is unchanged; they are folded into st.o when it rises and at
@@ -335,11 +370,9 @@ __device__ __forceinline__ void int8_chunk(const DecodeArgs& a, const WorkItem& 
       consume_point(cur.k[i][0]);
       consume_point(cur.k[i][1]);
     }
-#pragma unroll
-    for (int t = 0; t < kPageSize; ++t) consume_point(cur.v[t]);
     // ---- QK: exact integer dot products
     float s[kGroupPages];
-    float sv[kGroupPages];
+    float svu[kGroupPages];
 #pragma unroll
     for (int i = 0; i < kGroupPages; ++i) {
       v4i acc = {0, 0, 0, 0};
@@ -348,42 +381,45 @@ __device__ __forceinline__ void int8_chunk(const DecodeArgs& a, const WorkItem& 
       const int slot = g * kGroupPages + i;
       const int ls = min(slot, count - 1);
       const float sk = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, my_sk), ls));
-      sv[i] = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, my_sv), ls));
-      const bool valid = slot < count && !(slot == last_slot && m16 >= last_len);
-      s[i] = valid ? from_digits(acc) * (qscale * sk) : kNegInf;
+      svu[i] = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, my_svu), ls));
+      // visible tokens of this slot: 16, last_len on the segment's final
+      // page, 0 past the chunk end (uniform)
+      const int lim = slot < count ? (slot == last_slot ? last_len : kPageSize) : 0;
+      const float score = from_digits(acc) * (qscale * sk);
+      s[i] = m16 < lim ? score : kNegInf;
     }
     float p[kGroupPages];
-    const float alpha = softmax_update<kGroupPages>(st, s, p);
+    const float alpha = softmax_update_fast<kGroupPages>(st, s, p);
     if (__builtin_amdgcn_ballot_w64(alpha != 1.0f)) fold(alpha);
 
-    // ---- P digits -> LDS [page i][head kg][digit][token m16]
+    // ---- P digits: one dword per digit row holds this token's 4 pages
+    uint32_t y[4];
 #pragma unroll
-    for (int i = 0; i < kGroupPages; ++i) {
-      int d0, d1, d2;
-      three_digits(static_cast<int>(rintf(p[i] * sv[i] * p_unit)), d0, d1, d2);
-      uint8_t* row = lds + ((i * 4 + kg) * 4) * 16 + m16;
-      row[0] = static_cast<uint8_t>(d0);
-      row[16] = static_cast<uint8_t>(d1);
-      row[32] = static_cast<uint8_t>(d2);
-    }
+    for (int i = 0; i < kGroupPages; ++i) y[i] = digit_bytes(static_cast<int>(rintf(p[i] * svu[i])));
+    uint32_t dig[4];
+    transpose4x4(y, dig);          // dig[b] = digit byte b of pages 0..3
+    p_dst[0] = dig[2];             // row 4h:   d0 (weight 65536)
+    p_dst[4] = dig[1];             // row 4h+1: d1 (weight 256)
+    p_dst[8] = dig[0];             // row 4h+2: d2
     wave_lds_fence();
-    // A operand: lane (row 4h+c, page kg): 16 token digits
-    const v4i pa = *reinterpret_cast<const v4i*>(lds + ((kg * 4 + a_head) * 4 + a_digit) * 16);
+    const v4i pa = *p_src;
     wave_lds_fence();
 
-    // ---- PV: V code bytes transposed to token-major operands; n-block nb
-    // covers output dim 8*(lane%16) + nb
+    // ---- PV: V bytes of token 4*kg+t of the 4 pages transposed to one
+    // dword per output dim; n-block nb covers output dim 8*(lane%16) + nb
+#pragma unroll
+    for (int i = 0; i < 16; ++i) consume_point(cur.v[i]);
 #pragma unroll
     for (int half = 0; half < 2; ++half) {
-      uint32_t cols[4][4];   // [dim j][token quad]
+      uint32_t cols[4][4];   // [dim j][token t]
 #pragma unroll
-      for (int tq = 0; tq < 4; ++tq) {
-        const uint32_t r[4] = {cur.v[4 * tq][half], cur.v[4 * tq + 1][half], cur.v[4 * tq + 2][half],
-                               cur.v[4 * tq + 3][half]};
+      for (int t = 0; t < 4; ++t) {
+        const uint32_t r[4] = {cur.v[t][half], cur.v[4 + t][half], cur.v[8 + t][half],
+                               cur.v[12 + t][half]};
         uint32_t c[4];
         transpose4x4(r, c);
 #pragma unroll
-        for (int j = 0; j < 4; ++j) cols[j][tq] = c[j];
+        for (int j = 0; j < 4; ++j) cols[j][t] = c[j];
       }
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
@@ -396,8 +432,9 @@ __device__ __forceinline__ void int8_chunk(const DecodeArgs& a, const WorkItem& 
 
   // Software pipeline: the loads of group g+1 are in flight while group g is
   // computed; consume_point keeps the compiler from pulling g+1's uses (and
-  // their waits) into iteration g.  The steady-state loop has no branches
-  // around loads; the last one or two groups are peeled.
+  // their waits) into iteration g, and places the wait for V after QK and
+  // the softmax.  The steady-state loop has no branches around loads; the
+  // last one or two groups are peeled.
   int g = 0;
   for (; g + 2 < groups; g += 2) {
     issue(g + 1, buf[1]);
@@ -488,11 +525,11 @@ __device__ __forceinline__ void fp16_pages(const DecodeArgs& a, int request, con
     v4f acc = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
     for (int j = 0; j < 4; ++j) acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(qa[j], cur.k[j], acc, 0, 0, 0);
-    bool valid = true;
-    if (slot == last_slot && m16 >= last_len) valid = false;
-    float s[1] = {valid ? acc.x * a.sm_scale_log2 : kNegInf};
+    const int lim = slot == last_slot ? last_len : kPageSize;
+    const float score = acc.x * a.sm_scale_log2;
+    float s[1] = {m16 < lim ? score : kNegInf};
     float p[1];
-    const float alpha = softmax_update<1>(st, s, p);
+    const float alpha = softmax_update_fast<1>(st, s, p);
     if (__builtin_amdgcn_ballot_w64(alpha != 1.0f)) fold(alpha);
 
     // P as an FP16 hi/lo pair (p = hi + lo to ~22 bits) -> LDS [head][part][token];
@@ -550,6 +587,9 @@ __global__ __launch_bounds__(kWave * kMaxWavesPerBlock) void decode_partial_kern
   const int wave = threadIdx.x / kWave;
   const int lane = threadIdx.x % kWave;
   const int kv = blockIdx.y * a.waves_per_block + wave;
+#ifdef PG_TRACE_TIMES
+  const uint64_t t_entry = __builtin_amdgcn_s_memrealtime();
+#endif
   const WorkItem it = a.items[blockIdx.x];
   uint8_t* lds = lds_all + wave * kLdsPerWave;
   HeadState st;
@@ -582,6 +622,25 @@ __global__ __launch_bounds__(kWave * kMaxWavesPerBlock) void decode_partial_kern
     a.partial_m[row] = st.m;
     a.partial_l[row] = l_row;
   }
+#ifdef PG_TRACE_TIMES
+  // Timing builds only: wave timestamps replace dims 0..7 of query head
+  // 4*kv's partial row (the combined output is then meaningless).
+  const uint64_t t_end = __builtin_amdgcn_s_memrealtime();
+  if (lane == 0) {
+    const uint32_t hw_id = __builtin_amdgcn_s_getreg((31 << 11) | 4);
+    const uint32_t xcc_id = __builtin_amdgcn_s_getreg((31 << 11) | 20);
+    const int64_t row0 = (static_cast<int64_t>(it.request) * a.num_qo_heads + kv * kGqa) * a.max_items +
+                         it.item_in_request;
+    uint32_t* tr = reinterpret_cast<uint32_t*>(a.partial_o + row0 * kHeadDim);
+    tr[0] = static_cast<uint32_t>(t_entry);
+    tr[1] = static_cast<uint32_t>(t_entry >> 32);
+    tr[2] = static_cast<uint32_t>(t_end);
+    tr[3] = static_cast<uint32_t>(t_end >> 32);
+    tr[4] = hw_id;
+    tr[5] = xcc_id;
+    tr[6] = static_cast<uint32_t>(blockIdx.x);
+  }
+#endif
 }
 
 // ---------------------------------------------------------------------------
@@ -908,7 +967,7 @@ int32_t build_plan(const int32_t* host_indptr, const int32_t* host_last_page_len
     // thousand pages, 16-page chunks beat finer ones because each work
     // item pays a fixed start-up (page-table load, then the first group);
     // smaller problems use chunks down to one PV group for parallelism.
-    lo = hi >= 12.0 * static_cast<double>(target) ? 16.0 : 1e-3;
+    lo = hi >= 12.0 * static_cast<double>(target) ? kLargeBatchMinChunk : 1e-3;
     if (count_for(hi, nullptr) <= target) {
       for (int iter = 0; iter < 64; ++iter) {
         const double mid = 0.5 * (lo + hi);

@@ -92,7 +92,7 @@ class _Planned:
 
     def make_plan(self, host_indptr, host_last, primary_kind, host_tail_indptr, host_tail_last,
                   num_qo_heads, num_kv_heads, head_dim, page_size, split_pages, tail_split_pages,
-                  device) -> None:
+                  device, num_cus: Optional[int] = None) -> None:
         lib = _capi.library()
         batch = host_indptr.numel() - 1
         rc = lib.pg_decode_plan(
@@ -100,7 +100,7 @@ class _Planned:
             None if host_tail_indptr is None else host_tail_indptr.data_ptr(),
             None if host_tail_last is None else host_tail_last.data_ptr(),
             num_qo_heads, num_kv_heads, head_dim, page_size, int(split_pages or 0),
-            int(tail_split_pages or 0), _num_cus(device), self.workspace.data_ptr(),
+            int(tail_split_pages or 0), int(num_cus or _num_cus(device)), self.workspace.data_ptr(),
             self.workspace.numel(), ctypes.byref(self.plan), _stream())
         _capi.check(rc, "decode plan")
         self.planned = True
@@ -331,7 +331,9 @@ class PageGaugeSegmentedDecode:
              tail_last_page_len, num_qo_heads: int = HQ, num_kv_heads: int = HKV,
              head_dim: int = DIM, page_size: int = PAGE, sm_scale: Optional[float] = None,
              fixed_split_size: Optional[int] = None,
-             tail_split_size: Optional[int] = None) -> None:
+             tail_split_size: Optional[int] = None, num_cus: Optional[int] = None) -> None:
+        """``num_cus``: workgroups the balanced plan targets (default: the
+        device's CU count)."""
         for t, n in ((old_indices, "old_indices"), (old_last_page_len, "old_last_page_len"),
                      (tail_indices, "tail_indices"), (tail_last_page_len, "tail_last_page_len")):
             _check_index(t, n)
@@ -342,7 +344,7 @@ class PageGaugeSegmentedDecode:
         self._state.make_plan(host_old, _host_i32(old_last_page_len), _capi.PG_KV_INT8, host_tail,
                               _host_i32(tail_last_page_len), num_qo_heads, num_kv_heads, head_dim,
                               page_size, fixed_split_size or 0, tail_split_size or 0,
-                              old_indices.device)
+                              old_indices.device, num_cus)
         self._old = (old_indices, old_last_page_len)
         self._tail = (tail_indices, tail_last_page_len)
         self._batch = host_old.numel() - 1
