@@ -7,7 +7,7 @@
 
 #include <string>
 
-#include "../../include/pagegauge_hip.h"
+#include "pagegauge_hip.h"
 
 namespace pg {
 

@@ -229,12 +229,7 @@ __device__ __forceinline__ void int8_chunk(const DecodeArgs& a, const WorkItem& 
   const int groups = (count + kGroupPages - 1) / kGroupPages;
 
   // Chunk metadata, one lane per page slot: physical page and K/V page scales.
-#ifdef PG_PROBE_SAME_PAGE
-  // Timing builds only: every slot reads the chunk's first page (cache-resident).
-  const int my_page = a.indices[begin];
-#else
   const int my_page = a.indices[begin + min(lane, count - 1)];
-#endif
 
   // ---- query (A operand of QK): dims 16*kg + 64*j + b, b = 0..15
   const uint16_t* q = a.query + it.request * a.query_batch_stride +
@@ -267,18 +262,6 @@ __device__ __forceinline__ void int8_chunk(const DecodeArgs& a, const WorkItem& 
       kp[i] = kc + static_cast<int64_t>(page) * page_stride;
       vp[i] = vc + static_cast<int64_t>(page) * page_stride;
     }
-#ifdef PG_PROBE_NO_LOADS
-    // Timing builds only: synthetic operands, no K/V memory traffic.
-#pragma unroll
-    for (int i = 0; i < kGroupPages; ++i) {
-      const int page = static_cast<int>(reinterpret_cast<uintptr_t>(kp[i]) >> 14);
-      dst.k[i][0] = v4i{page ^ lane, page + lane, page * 3, lane * 5};
-      dst.k[i][1] = v4i{page ^ (lane << 3), page - lane, page * 7, lane * 9};
-#pragma unroll
-      for (int t = 0; t < 4; ++t)
-        dst.v[4 * i + t] = v2u{static_cast<uint32_t>(page * 31 + t + lane), static_cast<uint32_t>(page ^ (t << 4) ^ lane)};
-    }
-#else
 #pragma unroll
     for (int i = 0; i < kGroupPages; ++i) {
       dst.k[i][0] = *reinterpret_cast<const v4i*>(kp[i] + k_off);
@@ -289,7 +272,6 @@ __device__ __forceinline__ void int8_chunk(const DecodeArgs& a, const WorkItem& 
 #pragma unroll
       for (int t = 0; t < 4; ++t)
         dst.v[4 * i + t] = *reinterpret_cast<const v2u*>(vp[i] + v_off + t * row_stride);
-#endif
   };
   issue(0, buf[0]);
 
@@ -587,9 +569,6 @@ __global__ __launch_bounds__(kWave * kMaxWavesPerBlock) void decode_partial_kern
   const int wave = threadIdx.x / kWave;
   const int lane = threadIdx.x % kWave;
   const int kv = blockIdx.y * a.waves_per_block + wave;
-#ifdef PG_TRACE_TIMES
-  const uint64_t t_entry = __builtin_amdgcn_s_memrealtime();
-#endif
   const WorkItem it = a.items[blockIdx.x];
   uint8_t* lds = lds_all + wave * kLdsPerWave;
   HeadState st;
@@ -622,25 +601,6 @@ __global__ __launch_bounds__(kWave * kMaxWavesPerBlock) void decode_partial_kern
     a.partial_m[row] = st.m;
     a.partial_l[row] = l_row;
   }
-#ifdef PG_TRACE_TIMES
-  // Timing builds only: wave timestamps replace dims 0..7 of query head
-  // 4*kv's partial row (the combined output is then meaningless).
-  const uint64_t t_end = __builtin_amdgcn_s_memrealtime();
-  if (lane == 0) {
-    const uint32_t hw_id = __builtin_amdgcn_s_getreg((31 << 11) | 4);
-    const uint32_t xcc_id = __builtin_amdgcn_s_getreg((31 << 11) | 20);
-    const int64_t row0 = (static_cast<int64_t>(it.request) * a.num_qo_heads + kv * kGqa) * a.max_items +
-                         it.item_in_request;
-    uint32_t* tr = reinterpret_cast<uint32_t*>(a.partial_o + row0 * kHeadDim);
-    tr[0] = static_cast<uint32_t>(t_entry);
-    tr[1] = static_cast<uint32_t>(t_entry >> 32);
-    tr[2] = static_cast<uint32_t>(t_end);
-    tr[3] = static_cast<uint32_t>(t_end >> 32);
-    tr[4] = hw_id;
-    tr[5] = xcc_id;
-    tr[6] = static_cast<uint32_t>(blockIdx.x);
-  }
-#endif
 }
 
 // ---------------------------------------------------------------------------

@@ -1,7 +1,7 @@
 // Thread-local error text for the C ABI (pg_last_error).
 #include <string>
 
-#include "../../include/pagegauge_hip.h"
+#include "pagegauge_hip.h"
 
 namespace pg {
 
