@@ -7,8 +7,8 @@ INT8 page-affine pages + a 256-token FP16 exact tail), Mistral-7B layer shape
 (32 query / 8 KV heads, head_dim 128, 16-token pages), seeded N(0,1) K/V with
 x8 on 4 of 128 channels, randomly permuted physical page table.
 
-A step is one decode call: the INT8+tail partial kernel and the combine kernel
-(value center and base-2 LSE included).  Following the reference protocol
+A step is one decode call (``pg_decode_run``): the INT8+tail split-KV partial
+kernel and the combine kernel (value center and base-2 LSE included).  Following the reference protocol
 (scripts/benchmark_flashinfer_page_affine_int8.py:295-349, :651-655) each
 cold sample is preceded by an untimed scrub.  The reference scrubs with a
 256 MiB read-modify-write; on MI355X that leaves the 256 MB Infinity Cache
@@ -79,7 +79,7 @@ def summarize(values_ms):
 
 def call_samples(torch, bound, n, scrub=None):
     """Whole-call durations (ms): events recorded on the launch stream before
-    the partial kernel and after the combine kernel, plain launches.
+    and after the call, plain launches.
     ``scrub`` runs before every sample, outside the events; it also keeps the
     GPU busy while the host queues the timed launches."""
     ev = [[torch.cuda.Event(enable_timing=True) for _ in range(2)] for _ in range(n)]
@@ -87,8 +87,7 @@ def call_samples(torch, bound, n, scrub=None):
         if scrub is not None:
             scrub()
         ev[i][0].record()
-        bound.partial()
-        bound.combine()
+        bound()
         ev[i][1].record()
     torch.cuda.synchronize()
     return [a.elapsed_time(b) for a, b in ev]
@@ -331,7 +330,7 @@ def main() -> int:
             "split_pages": dec.split_pages,
             "tail_split_pages": dec.tail_split_pages,
             "work_items": dec.num_work_items,
-            "step": "one decode call (partial kernel + combine kernel) after an untimed read-only 1 GiB scrub",
+            "step": "one decode call (pg_decode_run) after an untimed read-only 1 GiB scrub",
         },
         "roofline": {
             "bound": "hbm",

@@ -202,7 +202,8 @@ int32_t pg_decode_plan(const int32_t* host_indptr, const int32_t* host_last_page
  * errors) without a device: fills *plan and, if items_out != NULL, the work
  * list as 8 int32 per item {request, kind (PG_KV_*), segment (0 primary,
  * 1 tail), page_begin, page_end (positions in indices/tail_indices), last
- * position of the segment, item index inside its request, 0}; item_ptr_out
+ * position of the segment, item index inside its request, items of the
+ * request}; item_ptr_out
  * (if != NULL) receives [B+1] offsets of each request's items.  Call once
  * with items_out NULL to learn plan->num_items.  For inspection and tests of
  * the scheduler; no reference counterpart (FlashInfer's plan info is opaque). */
@@ -251,6 +252,20 @@ int32_t pg_decode_run_partial(const pg_decode_plan_t* plan, const void* query,
                               const void* tail_k, const void* tail_v, const int32_t* tail_indices,
                               const int32_t* tail_last_len, float sm_scale, void* workspace,
                               void* stream);
+/* pg_decode_run with kernel timing: start_event / stop_event (hipEvent_t
+ * created with timing enabled) receive the begin timestamp of the partial
+ * kernel's dispatch and the end timestamp of the combine kernel's
+ * (hipExtLaunchKernelGGL), i.e. the GPU time of the call without the launch
+ * gap before it.  For benchmarks; no reference counterpart. */
+int32_t pg_decode_run_timed(const pg_decode_plan_t* plan, const void* query,
+                            int64_t query_batch_stride, const void* k_cache, const void* v_cache,
+                            const void* k_scale, const void* v_scale, const int32_t* indices,
+                            const int32_t* last_page_len, const void* tail_k, const void* tail_v,
+                            const int32_t* tail_indices, const int32_t* tail_last_len,
+                            const void* value_center, int64_t center_batch_stride, void* out,
+                            float* lse, float sm_scale, void* workspace, void* stream,
+                            void* start_event, void* stop_event);
+
 /* pg_decode_run_partial with kernel timing: start_event / stop_event
  * (hipEvent_t created with timing enabled, either may be NULL) receive the
  * partial kernel's own dispatch begin/end timestamps (hipExtLaunchKernelGGL),

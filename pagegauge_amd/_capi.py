@@ -71,6 +71,8 @@ PROTOTYPES = {
                                    _i32, _i32, ctypes.POINTER(DecodePlan), _p, _i64, _p]),
     "pg_decode_run": (_i32, [ctypes.POINTER(DecodePlan), _p, _i64, _p, _p, _p, _p, _p, _p, _p, _p,
                              _p, _p, _p, _i64, _p, _p, _f32, _p, _p]),
+    "pg_decode_run_timed": (_i32, [ctypes.POINTER(DecodePlan), _p, _i64, _p, _p, _p, _p, _p, _p,
+                                   _p, _p, _p, _p, _p, _i64, _p, _p, _f32, _p, _p, _p, _p]),
     "pg_decode_run_partial": (_i32, [ctypes.POINTER(DecodePlan), _p, _i64, _p, _p, _p, _p, _p, _p,
                                      _p, _p, _p, _p, _f32, _p, _p]),
     "pg_decode_run_partial_timed": (_i32, [ctypes.POINTER(DecodePlan), _p, _i64, _p, _p, _p, _p,

@@ -72,7 +72,7 @@ struct WorkItem {
   int32_t page_end;    // exclusive
   int32_t last_page;   // absolute index of the segment's final page for the request
   int32_t item_in_request;  // position of this item among its request's items
-  int32_t pad;
+  int32_t items_in_request; // number of items of the request
 };
 static_assert(sizeof(WorkItem) == 32, "work item layout");
 
@@ -557,52 +557,6 @@ __device__ __forceinline__ void fp16_pages(const DecodeArgs& a, int request, con
   fold(1.0f);
 }
 
-__device__ __forceinline__ void init_state(HeadState& st) {
-  st.m = kNegInf;
-  st.l = 0.0f;
-#pragma unroll
-  for (int i = 0; i < 8; ++i) st.o[i] = 0.0f;
-}
-
-__global__ __launch_bounds__(kWave * kMaxWavesPerBlock) void decode_partial_kernel(DecodeArgs a) {
-  __shared__ __attribute__((aligned(16))) uint8_t lds_all[kMaxWavesPerBlock * kLdsPerWave];
-  const int wave = threadIdx.x / kWave;
-  const int lane = threadIdx.x % kWave;
-  const int kv = blockIdx.y * a.waves_per_block + wave;
-  const WorkItem it = a.items[blockIdx.x];
-  uint8_t* lds = lds_all + wave * kLdsPerWave;
-  HeadState st;
-  init_state(st);
-  if (it.kind == PG_KV_INT8) {
-    if (a.num_kv_heads == 8)
-      int8_chunk<8 * kHeadDim>(a, it, kv, lane, lds, st);
-    else
-      int8_chunk<0>(a, it, kv, lane, lds, st);
-  } else if (it.segment == 0) {
-    fp16_pages(a, it.request, static_cast<const uint16_t*>(a.k_cache),
-               static_cast<const uint16_t*>(a.v_cache), a.indices, it.page_begin, it.page_end,
-               it.last_page, a.last_page_len[it.request], kv, lane, lds, st);
-  } else {
-    fp16_pages(a, it.request, a.tail_k, a.tail_v, a.tail_indices, it.page_begin, it.page_end,
-               it.last_page, a.tail_last_len[it.request], kv, lane, lds, st);
-  }
-  // partial write: lane (head l/16, n = l%16) owns dims 8n..8n+7.  Layout
-  // [request][qo head][item of the request][128] so a combine block reads one
-  // (request, head) as a contiguous run.
-  const float l_row = row16_sum(st.l);
-  const int qh = kv * kGqa + (lane >> 4);
-  const int n = lane & 15;
-  const int64_t row = (static_cast<int64_t>(it.request) * a.num_qo_heads + qh) * a.max_items +
-                      it.item_in_request;
-  float* o = a.partial_o + row * kHeadDim + 8 * n;
-  *reinterpret_cast<float4*>(o) = make_float4(st.o[0], st.o[1], st.o[2], st.o[3]);
-  *reinterpret_cast<float4*>(o + 4) = make_float4(st.o[4], st.o[5], st.o[6], st.o[7]);
-  if (n == 0) {
-    a.partial_m[row] = st.m;
-    a.partial_l[row] = l_row;
-  }
-}
-
 // ---------------------------------------------------------------------------
 // Combine: block (request*Hq + head, dim quarter); 256 threads = 32 item rows
 // x 8 float4 columns, so one pass loads 32 partials of 32 dims in parallel.
@@ -625,7 +579,7 @@ struct CombineArgs {
 };
 
 __device__ __forceinline__ float block_reduce(float v, float* scratch, bool is_max) {
-  const int wave = threadIdx.x / kWave;
+  const int wave = (threadIdx.x % kCombineThreads) / kWave;
   const int lane = threadIdx.x % kWave;
   v = is_max ? wave_max(v) : wave_sum(v);
   __syncthreads();
@@ -643,18 +597,28 @@ __device__ __forceinline__ void fma4(float4& acc, float w, const float4& v) {
   acc.w += w * v.w;
 }
 
-__global__ __launch_bounds__(kCombineThreads) void combine_kernel(CombineArgs a) {
-  __shared__ float scratch[kCombineThreads / kWave];
-  __shared__ float4 partial_acc[kCombineRows][kCombineCols];
-  __shared__ float partial_l[kCombineThreads / kWave];
-  const int row_head = blockIdx.x;
+// Shared memory of one combine unit (256 threads).
+struct CombineShared {
+  float scratch[kCombineThreads / kWave];
+  float4 partial_acc[kCombineRows][kCombineCols];
+  float partial_l[kCombineThreads / kWave];
+};
+
+// Merges the partials of (request, query head) for dims 32*quarter.. +31 and
+// writes out/lse.  ``tid`` in [0, 256); every thread of the block calls this
+// the same number of times (it contains block barriers); ``active`` false
+// runs the barriers only.
+__device__ __forceinline__ void combine_unit(const CombineArgs& a, int row_head, int quarter,
+                                             int tid, bool active, CombineShared& sh) {
+  float* scratch = sh.scratch;
+  auto& partial_acc = sh.partial_acc;
+  float* partial_l = sh.partial_l;
   const int request = row_head / a.num_qo_heads;
   const int qh = row_head % a.num_qo_heads;
-  const int count = a.item_ptr[request + 1] - a.item_ptr[request];
-  const int tid = threadIdx.x;
+  const int count = active ? a.item_ptr[request + 1] - a.item_ptr[request] : 0;
   const int r = tid / kCombineCols;
   const int c = tid % kCombineCols;
-  const int dim = 32 * blockIdx.y + 4 * c;
+  const int dim = 32 * quarter + 4 * c;
   const int64_t base = static_cast<int64_t>(row_head) * a.max_items;
   const float* pm = a.partial_m + base;
   const float* pl = a.partial_l + base;
@@ -698,7 +662,7 @@ __global__ __launch_bounds__(kCombineThreads) void combine_kernel(CombineArgs a)
   partial_acc[r][c] = acc;
   if (tid % kWave == 0) partial_l[tid / kWave] = lsum;
   __syncthreads();
-  if (tid < kCombineCols) {
+  if (active && tid < kCombineCols) {
     float4 total = partial_acc[0][tid];
     for (int k = 1; k < kCombineRows; ++k) {
       const float4 v = partial_acc[k][tid];
@@ -712,7 +676,7 @@ __global__ __launch_bounds__(kCombineThreads) void combine_kernel(CombineArgs a)
     const bool empty = !(l > 0.0f);
     const float inv = empty ? 0.0f : 1.0f / l;
     float o4[4] = {total.x * inv, total.y * inv, total.z * inv, total.w * inv};
-    const int d = 32 * blockIdx.y + 4 * tid;
+    const int d = 32 * quarter + 4 * tid;
     if (a.value_center != nullptr) {
       const uint16_t* cv = a.value_center + request * a.center_batch_stride + (qh / kGqa) * kHeadDim + d;
 #pragma unroll
@@ -721,8 +685,60 @@ __global__ __launch_bounds__(kCombineThreads) void combine_kernel(CombineArgs a)
     uint16_t* out = a.out + static_cast<int64_t>(row_head) * kHeadDim + d;
     *reinterpret_cast<__half2*>(out) = __floats2half2_rn(o4[0], o4[1]);
     *reinterpret_cast<__half2*>(out + 2) = __floats2half2_rn(o4[2], o4[3]);
-    if (tid == 0 && blockIdx.y == 0 && a.lse != nullptr)
+    if (active && tid == 0 && quarter == 0 && a.lse != nullptr)
       a.lse[row_head] = empty ? kNegInf : log2f(l) + m;
+  }
+  __syncthreads();   // the shared buffers are reused by the next unit
+}
+
+__global__ __launch_bounds__(kCombineThreads) void combine_kernel(CombineArgs a) {
+  __shared__ CombineShared sh;
+  combine_unit(a, blockIdx.x, blockIdx.y, threadIdx.x, true, sh);
+}
+
+__device__ __forceinline__ void init_state(HeadState& st) {
+  st.m = kNegInf;
+  st.l = 0.0f;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) st.o[i] = 0.0f;
+}
+
+__global__ __launch_bounds__(kWave * kMaxWavesPerBlock) void decode_partial_kernel(DecodeArgs a) {
+  __shared__ __attribute__((aligned(16))) uint8_t lds_all[kMaxWavesPerBlock * kLdsPerWave];
+  const int wave = threadIdx.x / kWave;
+  const int lane = threadIdx.x % kWave;
+  const int kv = blockIdx.y * a.waves_per_block + wave;
+  const WorkItem it = a.items[blockIdx.x];
+  uint8_t* lds = lds_all + wave * kLdsPerWave;
+  HeadState st;
+  init_state(st);
+  if (it.kind == PG_KV_INT8) {
+    if (a.num_kv_heads == 8)
+      int8_chunk<8 * kHeadDim>(a, it, kv, lane, lds, st);
+    else
+      int8_chunk<0>(a, it, kv, lane, lds, st);
+  } else if (it.segment == 0) {
+    fp16_pages(a, it.request, static_cast<const uint16_t*>(a.k_cache),
+               static_cast<const uint16_t*>(a.v_cache), a.indices, it.page_begin, it.page_end,
+               it.last_page, a.last_page_len[it.request], kv, lane, lds, st);
+  } else {
+    fp16_pages(a, it.request, a.tail_k, a.tail_v, a.tail_indices, it.page_begin, it.page_end,
+               it.last_page, a.tail_last_len[it.request], kv, lane, lds, st);
+  }
+  // partial write: lane (head l/16, n = l%16) owns dims 8n..8n+7.  Layout
+  // [request][qo head][item of the request][128] so a combine block reads one
+  // (request, head) as a contiguous run.
+  const float l_row = row16_sum(st.l);
+  const int qh = kv * kGqa + (lane >> 4);
+  const int n = lane & 15;
+  const int64_t row = (static_cast<int64_t>(it.request) * a.num_qo_heads + qh) * a.max_items +
+                      it.item_in_request;
+  float* o = a.partial_o + row * kHeadDim + 8 * n;
+  *reinterpret_cast<float4*>(o) = make_float4(st.o[0], st.o[1], st.o[2], st.o[3]);
+  *reinterpret_cast<float4*>(o + 4) = make_float4(st.o[4], st.o[5], st.o[6], st.o[7]);
+  if (n == 0) {
+    a.partial_m[row] = st.m;
+    a.partial_l[row] = l_row;
   }
 }
 
@@ -961,7 +977,9 @@ int32_t build_plan(const int32_t* host_indptr, const int32_t* host_last_page_len
         else tail_split_pages = std::max(tail_split_pages, size);
       }
     }
-    max_per_request = std::max(max_per_request, static_cast<int>(items.size()) - item_ptr[b]);
+    const int in_request = static_cast<int>(items.size()) - item_ptr[b];
+    for (size_t k = item_ptr[b]; k < items.size(); ++k) items[k].items_in_request = in_request;
+    max_per_request = std::max(max_per_request, in_request);
   }
   item_ptr[batch_size] = static_cast<int32_t>(items.size());
   if (max_per_request > kMaxItemsPerRequest)
@@ -1104,6 +1122,7 @@ int32_t launch_partial(const pg_decode_plan_t* plan, const void* query,
   if (!(sm_scale > 0.0f) || !__builtin_isfinite(sm_scale))
     return fail(PG_ERROR_INVALID_ARGUMENT, "sm_scale must be positive and finite");
   if (plan->num_items == 0) return PG_OK;
+  uint8_t* ws = static_cast<uint8_t*>(workspace);
   const PartialViews pv = partial_views(plan, workspace);
   DecodeArgs a{};
   a.query = static_cast<const uint16_t*>(query);
@@ -1118,7 +1137,7 @@ int32_t launch_partial(const pg_decode_plan_t* plan, const void* query,
   a.tail_v = static_cast<const uint16_t*>(tail_v);
   a.tail_indices = tail_indices;
   a.tail_last_len = tail_last_len;
-  a.items = reinterpret_cast<const WorkItem*>(static_cast<uint8_t*>(workspace) + plan->items_offset);
+  a.items = reinterpret_cast<const WorkItem*>(ws + plan->items_offset);
   a.partial_o = pv.o;
   a.partial_m = pv.m;
   a.partial_l = pv.l;
@@ -1138,6 +1157,49 @@ int32_t launch_partial(const pg_decode_plan_t* plan, const void* query,
                        as_stream(stream), a);
   }
   return check_launch("decode_partial");
+}
+
+int32_t launch_combine(const pg_decode_plan_t* plan, const void* value_center,
+                       int64_t center_batch_stride, void* out, float* lse, void* workspace,
+                       void* stream, void* stop_event) {
+  clear_error();
+  if (!plan || !out || !workspace) return fail(PG_ERROR_INVALID_ARGUMENT, "null run argument");
+  const PartialViews pv = partial_views(plan, workspace);
+  CombineArgs c{};
+  c.partial_o = pv.o;
+  c.partial_m = pv.m;
+  c.partial_l = pv.l;
+  c.item_ptr = reinterpret_cast<const int32_t*>(static_cast<uint8_t*>(workspace) +
+                                                plan->item_ptr_offset);
+  c.value_center = static_cast<const uint16_t*>(value_center);
+  c.center_batch_stride = center_batch_stride;
+  c.out = static_cast<uint16_t*>(out);
+  c.lse = lse;
+  c.num_qo_heads = plan->num_qo_heads;
+  c.max_items = std::max(1, plan->max_items_per_request);
+  const dim3 grid(plan->batch_size * plan->num_qo_heads, kHeadDim / 32);
+  if (stop_event) {
+    hipExtLaunchKernelGGL(combine_kernel, grid, dim3(kCombineThreads), 0, as_stream(stream),
+                          nullptr, static_cast<hipEvent_t>(stop_event), 0, c);
+  } else {
+    hipLaunchKernelGGL(combine_kernel, grid, dim3(kCombineThreads), 0, as_stream(stream), c);
+  }
+  return check_launch("decode_combine");
+}
+
+int32_t run_decode(const pg_decode_plan_t* plan, const void* query, int64_t query_batch_stride,
+                   const void* k_cache, const void* v_cache, const void* k_scale,
+                   const void* v_scale, const int32_t* indices, const int32_t* last_page_len,
+                   const void* tail_k, const void* tail_v, const int32_t* tail_indices,
+                   const int32_t* tail_last_len, const void* value_center,
+                   int64_t center_batch_stride, void* out, float* lse, float sm_scale,
+                   void* workspace, void* stream, void* start_event, void* stop_event) {
+  if (int32_t rc = launch_partial(plan, query, query_batch_stride, k_cache, v_cache, k_scale,
+                                  v_scale, indices, last_page_len, tail_k, tail_v, tail_indices,
+                                  tail_last_len, sm_scale, workspace, stream, start_event, nullptr))
+    return rc;
+  return launch_combine(plan, value_center, center_batch_stride, out, lse, workspace, stream,
+                        stop_event);
 }
 
 }  // namespace
@@ -1169,24 +1231,8 @@ extern "C" int32_t pg_decode_run_partial_timed(
 extern "C" int32_t pg_decode_run_combine(const pg_decode_plan_t* plan, const void* value_center,
                                          int64_t center_batch_stride, void* out, float* lse,
                                          void* workspace, void* stream) {
-  clear_error();
-  if (!plan || !out || !workspace) return fail(PG_ERROR_INVALID_ARGUMENT, "null run argument");
-  const PartialViews pv = partial_views(plan, workspace);
-  CombineArgs c{};
-  c.partial_o = pv.o;
-  c.partial_m = pv.m;
-  c.partial_l = pv.l;
-  c.item_ptr = reinterpret_cast<const int32_t*>(static_cast<uint8_t*>(workspace) +
-                                                plan->item_ptr_offset);
-  c.value_center = static_cast<const uint16_t*>(value_center);
-  c.center_batch_stride = center_batch_stride;
-  c.out = static_cast<uint16_t*>(out);
-  c.lse = lse;
-  c.num_qo_heads = plan->num_qo_heads;
-  c.max_items = std::max(1, plan->max_items_per_request);
-  hipLaunchKernelGGL(combine_kernel, dim3(plan->batch_size * plan->num_qo_heads, kHeadDim / 32),
-                     dim3(kCombineThreads), 0, as_stream(stream), c);
-  return check_launch("decode_combine");
+  return launch_combine(plan, value_center, center_batch_stride, out, lse, workspace, stream,
+                        nullptr);
 }
 
 extern "C" int32_t pg_decode_run(const pg_decode_plan_t* plan, const void* query,
@@ -1197,12 +1243,25 @@ extern "C" int32_t pg_decode_run(const pg_decode_plan_t* plan, const void* query
                                  const int32_t* tail_indices, const int32_t* tail_last_len,
                                  const void* value_center, int64_t center_batch_stride, void* out,
                                  float* lse, float sm_scale, void* workspace, void* stream) {
-  if (int32_t rc = pg_decode_run_partial(plan, query, query_batch_stride, k_cache, v_cache,
-                                         k_scale, v_scale, indices, last_page_len, tail_k, tail_v,
-                                         tail_indices, tail_last_len, sm_scale, workspace, stream))
-    return rc;
-  return pg_decode_run_combine(plan, value_center, center_batch_stride, out, lse, workspace,
-                               stream);
+  return run_decode(plan, query, query_batch_stride, k_cache, v_cache, k_scale, v_scale, indices,
+                    last_page_len, tail_k, tail_v, tail_indices, tail_last_len, value_center,
+                    center_batch_stride, out, lse, sm_scale, workspace, stream, nullptr, nullptr);
+}
+
+extern "C" int32_t pg_decode_run_timed(const pg_decode_plan_t* plan, const void* query,
+                                       int64_t query_batch_stride, const void* k_cache,
+                                       const void* v_cache, const void* k_scale,
+                                       const void* v_scale, const int32_t* indices,
+                                       const int32_t* last_page_len, const void* tail_k,
+                                       const void* tail_v, const int32_t* tail_indices,
+                                       const int32_t* tail_last_len, const void* value_center,
+                                       int64_t center_batch_stride, void* out, float* lse,
+                                       float sm_scale, void* workspace, void* stream,
+                                       void* start_event, void* stop_event) {
+  return run_decode(plan, query, query_batch_stride, k_cache, v_cache, k_scale, v_scale, indices,
+                    last_page_len, tail_k, tail_v, tail_indices, tail_last_len, value_center,
+                    center_batch_stride, out, lse, sm_scale, workspace, stream, start_event,
+                    stop_event);
 }
 
 extern "C" int32_t pg_merge_state_in_place(void* v, float* s, const void* v_other,

@@ -115,7 +115,7 @@ class _Planned:
 
 
 WORK_ITEM_FIELDS = ("request", "kind", "segment", "page_begin", "page_end", "last_page",
-                    "item_in_request", "pad")
+                    "item_in_request", "items_in_request")
 
 
 def plan_work_items(indptr, last_page_len, tail_indptr=None, tail_last_page_len=None,
@@ -151,11 +151,14 @@ def plan_work_items(indptr, last_page_len, tail_indptr=None, tail_last_page_len=
 
 
 class BoundDecode:
-    """A planned decode with every pointer resolved: ``partial()``,
-    ``combine()`` and ``__call__`` (both) issue the launches with no tensor
-    validation, for serving loops and timing.  The bound tensors must stay
-    alive and keep their storage; ``stream`` is a raw hipStream_t handle
-    (default: the current stream when ``bind`` was called)."""
+    """A planned decode with every pointer resolved, for serving loops and
+    timing: ``__call__`` issues the call (``pg_decode_run``: the partial and
+    the combine kernels), ``partial()`` / ``combine()`` the two kernels
+    separately, and ``timed(start, stop)`` the call with two timing events
+    stamped by its first and last kernel dispatches.  No tensor validation
+    happens here; the bound tensors must stay alive and keep their storage.
+    ``stream`` is a raw hipStream_t handle (default: the current stream when
+    ``bind`` was called)."""
 
     def __init__(self, state: "_Planned", partial_args: tuple, combine_args: tuple,
                  stream: int) -> None:
@@ -165,8 +168,14 @@ class BoundDecode:
         self._partial = lib.pg_decode_run_partial
         self._partial_timed = lib.pg_decode_run_partial_timed
         self._combine = lib.pg_decode_run_combine
-        self._partial_args = (self._plan_ref, *partial_args, state.workspace.data_ptr(), stream)
-        self._combine_args = (self._plan_ref, *combine_args, state.workspace.data_ptr(), stream)
+        self._run = lib.pg_decode_run
+        self._run_timed = lib.pg_decode_run_timed
+        ws = state.workspace.data_ptr()
+        self._partial_args = (self._plan_ref, *partial_args, ws, stream)
+        self._combine_args = (self._plan_ref, *combine_args, ws, stream)
+        # pg_decode_run: partial inputs (without sm_scale), combine outputs, sm_scale
+        self._run_args = (self._plan_ref, *partial_args[:-1], *combine_args, partial_args[-1], ws,
+                          stream)
 
     def partial(self) -> None:
         rc = self._partial(*self._partial_args)
@@ -187,9 +196,15 @@ class BoundDecode:
         if rc:
             _capi.check(rc, "decode combine")
 
+    def timed(self, start_event: int, stop_event: int) -> None:
+        rc = self._run_timed(*self._run_args, start_event, stop_event)
+        if rc:
+            _capi.check(rc, "decode run")
+
     def __call__(self) -> None:
-        self.partial()
-        self.combine()
+        rc = self._run(*self._run_args)
+        if rc:
+            _capi.check(rc, "decode run")
 
 
 class BatchDecodeWithPagedKVCacheWrapper:
@@ -220,7 +235,7 @@ class BatchDecodeWithPagedKVCacheWrapper:
              kv_data_type=None, o_data_type=None, data_type=None, sm_scale=None,
              rope_scale=None, rope_theta=None, non_blocking: bool = True,
              fixed_split_size: Optional[int] = None, disable_split_kv: bool = False,
-             **_unused) -> None:
+             num_cus: Optional[int] = None, **_unused) -> None:
         if pos_encoding_mode != "NONE":
             raise ValueError("only pos_encoding_mode='NONE' is supported")
         if window_left not in (-1, None) or logits_soft_cap not in (None, 0.0):
@@ -237,7 +252,7 @@ class BatchDecodeWithPagedKVCacheWrapper:
         kind = _capi.PG_KV_INT8 if kv_dtype == torch.int8 else _capi.PG_KV_FP16
         split = 1 << 30 if disable_split_kv else (fixed_split_size or 0)
         self._state.make_plan(host_indptr, host_last, kind, None, None, num_qo_heads, num_kv_heads,
-                              head_dim, page_size, split, 0, indices.device)
+                              head_dim, page_size, split, 0, indices.device, num_cus)
         self._indices = indices
         self._last_page_len = last_page_len
         self._kv_dtype = kv_dtype

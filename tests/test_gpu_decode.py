@@ -249,3 +249,34 @@ def test_empty_request_gives_center_and_neg_inf_lse(cuda, workspace):
     torch.cuda.synchronize()
     assert torch.equal(out, center.repeat_interleave(4, dim=1))
     assert bool(torch.isneginf(lse).all())
+
+
+def test_bound_timed_call_equals_plain_call(cuda, workspace):
+    """pg_decode_run_timed (dispatch-stamped events) computes exactly what
+    pg_decode_run does, and its events measure a positive GPU time."""
+    from pagegauge_amd import decode, workloads
+
+    w = workloads.build_decode_workload([4096, 1024], seed=20260844, device=cuda)
+    dec = decode.PageGaugeSegmentedDecode(workspace)
+    dec.plan(w.old_indptr, w.old_indices, w.old_last_page_len, w.tail_indptr, w.tail_indices,
+             w.tail_last_page_len)
+    outs = []
+    for timed in (False, True):
+        out = torch.full_like(w.query, float("nan"))
+        lse = torch.full((w.batch, 32), float("nan"), dtype=torch.float32, device=cuda)
+        bound = dec.bind(w.query, (w.k_codes, w.v_codes), w.k_scale, w.v_scale,
+                         (w.tail_k, w.tail_v), w.value_center, out=out, lse=lse)
+        if timed:
+            start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            start.record()
+            stop.record()
+            torch.cuda.synchronize()
+            bound.timed(start.cuda_event, stop.cuda_event)
+            torch.cuda.synchronize()
+            assert start.elapsed_time(stop) > 0.0
+        else:
+            bound()
+            torch.cuda.synchronize()
+        outs.append((cpu(out), cpu(lse)))
+    assert np.array_equal(outs[0][0].view(np.uint16), outs[1][0].view(np.uint16))
+    assert np.array_equal(outs[0][1].view(np.uint32), outs[1][1].view(np.uint32))

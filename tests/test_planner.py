@@ -30,6 +30,7 @@ def _check_cover(items, item_ptr, old_counts, tail_counts):
         mine = items[item_ptr[b]:item_ptr[b + 1]]
         assert (mine[:, 0] == b).all()
         assert list(mine[:, 6]) == list(range(len(mine)))          # item_in_request
+        assert (mine[:, 7] == len(mine)).all()                     # items_in_request
         for seg, ptr in ((0, old_ptr), (1, tail_ptr)):
             rows = mine[mine[:, 2] == seg]
             covered = sorted(p for r in rows for p in range(r[3], r[4]))
@@ -96,3 +97,4 @@ def test_fp16_primary_plan_has_no_tail_weighting():
 def test_plan_rejects_too_many_items_per_request():
     with pytest.raises(RuntimeError, match="too many splits"):
         plan_work_items([0, 5000], [16], split_pages=1)
+
