@@ -55,6 +55,8 @@ def parse_args() -> argparse.Namespace:
     p.add_argument("--cpu-seconds", type=float, default=12.0, help="CPU-baseline time budget")
     p.add_argument("--no-cpu", action="store_true")
     p.add_argument("--no-fp16", action="store_true")
+    p.add_argument("--no-configs", action="store_true",
+                   help="skip the config-1/3 decode lines and the config-4 update timing")
     p.add_argument("--sweep", default="", help="comma list of split sizes to time (pilot sweep)")
     p.add_argument("--modes", default="cold_clean,cold_rmw,hot",
                    help="cache states to time (cold_clean is required: it gives value/roofline)")
@@ -184,6 +186,113 @@ def committed_traffic(root: Path):
     return None
 
 
+def decode_config(torch, decode, w, scrub, samples: int):
+    """Cold (clean-scrub) call p50 and partial-kernel mean of one workload."""
+    ws = torch.empty(64 << 20, dtype=torch.uint8, device=w.query.device)
+    out = torch.empty_like(w.query)
+    lse = torch.empty(w.batch, 32, dtype=torch.float32, device=w.query.device)
+    dec = decode.PageGaugeSegmentedDecode(ws)
+    dec.plan(w.old_indptr, w.old_indices, w.old_last_page_len, w.tail_indptr, w.tail_indices,
+             w.tail_last_page_len)
+    bound = dec.bind(w.query, (w.k_codes, w.v_codes), w.k_scale, w.v_scale,
+                     (w.tail_k, w.tail_v), w.value_center, out=out, lse=lse)
+    for _ in range(3):
+        scrub()
+        bound()
+    kernel, call = timed_calls(torch, bound, samples, scrub=scrub)
+    kernel_us = 1e3 * statistics.fmean(kernel)
+    alg = w.algorithmic_bytes()
+    return {
+        "lengths": w.lengths if len(w.lengths) <= 8 else len(w.lengths),
+        "work_items": dec.num_work_items,
+        "call_p50_us": round(1e3 * statistics.median(call), 3),
+        "kernel_mean_us": round(kernel_us, 3),
+        "algorithmic_bytes": alg,
+        "achieved_gbps": round(alg / (kernel_us * 1e-6) / 1e9, 1),
+        "frac_of_peak": round(alg / (kernel_us * 1e-6) / 1e9 / HBM_PEAK_GBPS, 4),
+    }
+
+
+def update_config4(torch, device, replays: int):
+    """Config 4 cache update: B=8, 16 decode steps (start lengths
+    4096, 4099, ..., 16398: every row closes one page, four of them mid-window),
+    RoPE theta 1e6 at position = current length.  The 16 steps are captured in
+    a HIP graph and replayed back to back; reported as GPU µs per step for the
+    fused RoPE + centered append + finalize kernel (per-request positions),
+    the centered append + finalize without RoPE, and the plain FP16 append
+    (the reference's incremental-cost baseline,
+    scripts/benchmark_page_gauge_overheads.py:86-205)."""
+    from oracle import pg_oracle as oracle
+    from pagegauge_amd import runtime, update
+
+    ext = runtime.load_append_extension()
+    gen = torch.Generator().manual_seed(20260840)
+    start = [4096, 4099, 8192, 8199, 12288, 12299, 16384, 16398]
+    batch, ring, steps = 8, 16, 16
+    code_pages = (max(start) + steps + 15) // 16
+    cos_np, sin_np = oracle.rope_tables(max(start) + steps)
+    cos, sin = torch.from_numpy(cos_np).to(device), torch.from_numpy(sin_np).to(device)
+    rnd = lambda *shape, s=1.0: (torch.randn(*shape, generator=gen) * s).half().to(device)  # noqa: E731
+    kc, vc = rnd(batch, 8, 128, s=0.1), rnd(batch, 8, 128, s=0.1)
+    kc_shared, vc_shared = kc[0].contiguous(), vc[0].contiguous()
+    q = [rnd(batch, 32, 128) for _ in range(steps)]
+    k = [rnd(batch, 8, 128) for _ in range(steps)]
+    v = [rnd(batch, 8, 128) for _ in range(steps)]
+    pos = [torch.tensor([x + t for x in start], dtype=torch.int32, device=device) for t in range(steps)]
+    # per-request (page id, offset) of a request-major FP16 / exact pool
+    page_ids = [torch.tensor([r * code_pages + (x + t) // 16 for r, x in enumerate(start)],
+                             dtype=torch.int32, device=device) for t in range(steps)]
+    offsets = [torch.tensor([(x + t) % 16 for x in start], dtype=torch.int32, device=device)
+               for t in range(steps)]
+    exact = [rnd(batch * ring, 16, 8, 128) for _ in range(2)]
+    codes = [torch.zeros(batch * code_pages, 16, 8, 128, dtype=torch.int8, device=device) for _ in range(2)]
+    scales = [torch.zeros(batch * code_pages, 8, dtype=torch.float16, device=device) for _ in range(2)]
+    pool = [rnd(batch * code_pages, 16, 8, 128) for _ in range(2)]
+    rq = torch.zeros(batch, 32, 128, dtype=torch.float16, device=device)
+
+    def fused():
+        for t in range(steps):
+            ext.rope_append_page_gauge_positions(q[t], k[t], v[t], cos, sin, pos[t], kc, vc, rq,
+                                                 exact[0], exact[1], codes[0], codes[1],
+                                                 scales[0], scales[1], 0)
+
+    def finalize():
+        for t in range(steps):
+            update.append_finalize_page_gauge(k[t], v[t], kc_shared, vc_shared, pool[0], pool[1],
+                                              codes[0], codes[1], scales[0], scales[1],
+                                              page_ids[t], offsets[t])
+
+    def fp16():
+        for t in range(steps):
+            update.append_kv(k[t], v[t], pool[0], pool[1], page_ids[t], offsets[t])
+
+    result = {"batch": batch, "steps_per_graph": steps, "replays": replays,
+              "closing_rows_per_window": 8}
+    stream = torch.cuda.Stream()
+    for name, fn in (("fused_rope_append_finalize", fused), ("append_finalize", finalize),
+                     ("fp16_append", fp16)):
+        stream.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(stream):
+            fn()                                   # eager warm-up on the capture stream
+        torch.cuda.synchronize()
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph, stream=stream):
+            fn()
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(replays):
+            graph.replay()
+        e1.record()
+        torch.cuda.synchronize()
+        result[name + "_us_per_step"] = round(1e3 * e0.elapsed_time(e1) / (replays * steps), 3)
+    result["incremental_us_per_step"] = round(result["append_finalize_us_per_step"] -
+                                              result["fp16_append_us_per_step"], 3)
+    return result
+
+
 def cpu_baseline(w, budget_s: float):
     """C oracle dense decode of the same inputs, one host thread."""
     from oracle import c_oracle
@@ -291,6 +400,19 @@ def main() -> int:
         sweep[str(split)] = {"items": d2.num_work_items, "kernel_p50_us": 1e3 * statistics.median(k_ms),
                              "call_p50_us": 1e3 * statistics.median(c_ms)}
 
+    other = None
+    if not args.no_configs:
+        other = {"config1_b1_4k": decode_config(torch, decode, workloads.single_4k(args.seed, device=device),
+                                                scrub_clean, 30)}
+        ragged = {}
+        for seed in workloads.VALIDATION_SEEDS[:3]:
+            wr = workloads.b8_ragged(seed, device=device)
+            ragged[str(seed)] = decode_config(torch, decode, wr, scrub_clean, 30)
+            del wr
+            torch.cuda.empty_cache()
+        other["config3_b8_ragged"] = ragged
+        other["config4_update"] = update_config4(torch, device, 50)
+
     cpu = None
     parity = None
     if not args.no_cpu:
@@ -353,6 +475,7 @@ def main() -> int:
             for mode in ("cold_clean_1gib", "cold_rmw_256mib", "hot") if mode in int8},
         "parity_vs_oracle": parity,
         "split_sweep": sweep or None,
+        "other_configs": other,
         "wall_s_timed_region": round(wall_s, 3),
         "setup_s": round(setup_s, 2),
         "device": torch.cuda.get_device_name(device),
