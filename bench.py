@@ -29,6 +29,7 @@ from __future__ import annotations
 
 import argparse
 import json
+import math
 import os
 import statistics
 import sys
@@ -58,6 +59,10 @@ def parse_args() -> argparse.Namespace:
     p.add_argument("--no-configs", action="store_true",
                    help="skip the config-1/3 decode lines and the config-4 update timing")
     p.add_argument("--sweep", default="", help="comma list of split sizes to time (pilot sweep)")
+    p.add_argument("--no-decoder", action="store_true", help="skip the config-5 decoder line")
+    p.add_argument("--decoder-only", action="store_true",
+                   help="run only the config-5 decoder and print its JSON")
+    p.add_argument("--decoder-repeats", type=int, default=5)
     p.add_argument("--modes", default="cold_clean,cold_rmw,hot",
                    help="cache states to time (cold_clean is required: it gives value/roofline)")
     p.add_argument("--pmc-calls", type=int, default=0,
@@ -293,6 +298,102 @@ def update_config4(torch, device, replays: int):
     return result
 
 
+def decoder_config5(torch, device, repeats: int, context: int = 16384, steps: int = 16,
+                    seed: int = 20260850):
+    """Config 5: random-init Mistral-7B-shaped decoder, B=1, ``context``-token
+    prefill of uniform random ids, then ``steps`` greedy tokens with every
+    layer on the INT8 paged KV + FP16 tail (K2 append + K1 decode), each step
+    one HIP graph.  Reports ms/token and tokens/s of the PageGauge decoder and
+    of the same decoder over an FP16 cache, and the reference's logit gate
+    (cosine >= 0.995, top-1 agreement, max-abs;
+    scripts/benchmark_page_gauge_transformer.py:3865-3903) on a teacher-forced
+    sequence of random tokens."""
+    import torch.nn.functional as F
+
+    from pagegauge_amd import decoder as dec
+
+    t0 = time.perf_counter()
+    cfg = dec.DecoderConfig()
+    weights = dec.DecoderWeights(cfg, seed, device=device)
+    gen = torch.Generator().manual_seed(seed)
+    prompt = torch.randint(0, cfg.vocab, (context,), generator=gen)
+    forced = torch.randint(0, cfg.vocab, (steps,), generator=gen).to(device)
+    torch.cuda.synchronize()
+    t1 = time.perf_counter()
+    first, _, decoders = dec.build_decoders(weights, prompt, steps + 1)
+    torch.cuda.synchronize()
+    t2 = time.perf_counter()
+    result = {"model": "Mistral-7B architecture, random-init fp16 (32 layers, hidden 4096, "
+                       "32/8 heads, MLP 14336, vocab 32768)",
+              "prefill_tokens": context, "decode_steps": steps, "repeats": repeats,
+              "weights_init_s": round(t1 - t0, 2), "prefill_and_cache_build_s": round(t2 - t1, 2)}
+    kv_bytes = {}
+    per_layer_pages = math.ceil((context + steps) / 16)
+    kv_bytes["page_gauge"] = cfg.layers * ((per_layer_pages - 16) * (2 * 16 * 8 * 128 + 4 * 8)
+                                           + 16 * 2 * 16 * 8 * 256 + 2 * 8 * 128 * 2)
+    kv_bytes["fp16"] = cfg.layers * per_layer_pages * 2 * 16 * 8 * 256
+    weight_bytes = weights.bytes_per_token()
+    logits = {}
+    for name, d in decoders.items():
+        d.generate(first, context, steps, use_graphs=True)          # capture + warm
+        torch.cuda.synchronize()
+        walls, gpu = [], []
+        tokens_ref = None
+        for _ in range(repeats):
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            torch.cuda.synchronize()
+            w0 = time.perf_counter()
+            e0.record()
+            toks, _ = d.generate(first, context, steps, use_graphs=True)
+            e1.record()
+            torch.cuda.synchronize()
+            walls.append(time.perf_counter() - w0)
+            gpu.append(e0.elapsed_time(e1) * 1e-3)
+            tokens_ref = toks if tokens_ref is None else tokens_ref
+            if not torch.equal(toks, tokens_ref):
+                raise RuntimeError("greedy decode is not deterministic across repeats")
+        # eager (no graph) once, for the launch-overhead comparison
+        d.drop_graphs()
+        torch.cuda.synchronize()
+        w0 = time.perf_counter()
+        d.generate(first, context, steps, use_graphs=False)
+        torch.cuda.synchronize()
+        eager_s = time.perf_counter() - w0
+        ms_token = 1e3 * statistics.median(walls) / steps
+        total_bytes = weight_bytes + kv_bytes[name]
+        result[name] = {
+            "ms_per_token_wall_p50": round(ms_token, 4),
+            "ms_per_token_gpu_p50": round(1e3 * statistics.median(gpu) / steps, 4),
+            "tokens_per_s": round(1e3 / ms_token, 2),
+            "eager_ms_per_token": round(1e3 * eager_s / steps, 3),
+            "bytes_per_token": total_bytes,
+            "achieved_gbps": round(total_bytes / (ms_token * 1e-3) / 1e9, 1),
+            "hbm_frac": round(total_bytes / (ms_token * 1e-3) / 1e9 / HBM_PEAK_GBPS, 4),
+            "greedy_tokens": [int(t) for t in tokens_ref.reshape(-1).tolist()],
+        }
+        # teacher-forced logits for the comparison
+        seq = []
+        for i in range(steps):
+            seq.append(d.step(forced[i:i + 1], context + i).clone())
+        logits[name] = seq
+        del d
+    if "page_gauge" in logits and "fp16" in logits:
+        cos = [float(F.cosine_similarity(a, b, dim=-1).min())
+               for a, b in zip(logits["page_gauge"], logits["fp16"])]
+        top1 = [bool((a.argmax(-1) == b.argmax(-1)).all())
+                for a, b in zip(logits["page_gauge"], logits["fp16"])]
+        max_abs = max(float((a - b).abs().max()) for a, b in zip(logits["page_gauge"], logits["fp16"]))
+        result["page_gauge_vs_fp16_logits"] = {
+            "min_cosine": round(min(cos), 6), "top1_agreement": sum(top1) / len(top1),
+            "max_abs": round(max_abs, 5), "gate": "cosine >= 0.995 (reference default)",
+            "passed": min(cos) >= 0.995}
+        result["speedup_vs_fp16_cache"] = round(result["fp16"]["ms_per_token_wall_p50"]
+                                                / result["page_gauge"]["ms_per_token_wall_p50"], 4)
+    del decoders, weights
+    torch.cuda.empty_cache()
+    return result
+
+
 def cpu_baseline(w, budget_s: float):
     """C oracle dense decode of the same inputs, one host thread."""
     from oracle import c_oracle
@@ -331,6 +432,9 @@ def main() -> int:
         return 1
     device = torch.device("cuda:0")
     torch.cuda.set_device(device)
+    if args.decoder_only:
+        print(json.dumps(decoder_config5(torch, device, args.decoder_repeats)), flush=True)
+        return 0
     t_setup = time.perf_counter()
     w = workloads.b1_49k(args.seed, device=device, with_fp16_copy=not args.no_fp16)
     torch.cuda.synchronize()
@@ -412,6 +516,9 @@ def main() -> int:
             torch.cuda.empty_cache()
         other["config3_b8_ragged"] = ragged
         other["config4_update"] = update_config4(torch, device, 50)
+    if not args.no_decoder:
+        other = other or {}
+        other["config5_decoder"] = decoder_config5(torch, device, args.decoder_repeats)
 
     cpu = None
     parity = None

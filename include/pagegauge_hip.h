@@ -137,6 +137,40 @@ int32_t pg_quantize_completed_kv_pages(const void* key, const void* value,
                                        void* key_scales, void* value_scales,
                                        int64_t num_pages, int32_t heads, void* stream);
 
+/* Prefill cache population of one (layer, request): the bulk quantizer above
+ * plus the centered FP16 exact pages, in one launch.  Replaces the body of
+ * populate_backend_cache_layer (diagnostics/benchmark_backend_exclusive.py:442-506)
+ * and the per-page copies of build_caches
+ * (scripts/benchmark_page_gauge_transformer.py:1215-1245).
+ *   key/value: token-major prefix [pages*16, H, 128] fp16 whose token rows are
+ *     key_token_stride / value_token_stride elements apart (>= H*128, even;
+ *     e.g. a K/V slice of a fused QKV projection);
+ *   codes [pages,16,H,128] int8 and scales [pages,H] fp16 receive every page;
+ *   exact_page_map: optional int32[pages]; page i is also written as
+ *     fp16(f32(x) - f32(center)) to ring page exact_page_map[i] of
+ *     exact_key_pages / exact_value_pages ([*,16,H,128] fp16) when >= 0. */
+int32_t pg_prefill_page_gauge(const void* key, int64_t key_token_stride, const void* value,
+                              int64_t value_token_stride, const void* key_center,
+                              const void* value_center, int8_t* key_codes, int8_t* value_codes,
+                              void* key_scales, void* value_scales,
+                              const int32_t* exact_page_map, void* exact_key_pages,
+                              void* exact_value_pages, int64_t num_pages, int32_t heads,
+                              void* stream);
+
+/* Per-(head, dim) channel centers of a token-major K/V prefix: replaces
+ * token_major_centers (diagnostics/benchmark_backend_exclusive.py:372-395) and
+ * the center lines of build_caches (scripts/benchmark_page_gauge_transformer.py:1201-1214),
+ * `x.float().mean(dim=tokens).half()`.  The float32 reduction order of the
+ * reference is unspecified; here the sum is exact (int64 multiples of 2^-24),
+ * and the center is f16(f32(f64(sum)/tokens)), independent of order.
+ * tokens <= 2^22.  Workspace: pg_token_major_centers_workspace_bytes bytes of
+ * device memory, caller-owned; two launches, no allocation, no memset. */
+int64_t pg_token_major_centers_workspace_bytes(int64_t tokens, int32_t heads);
+int32_t pg_token_major_centers(const void* key, int64_t key_token_stride, const void* value,
+                               int64_t value_token_stride, int64_t tokens, int32_t heads,
+                               void* key_center, void* value_center, void* workspace,
+                               int64_t workspace_bytes, void* stream);
+
 /* ------------------------------------------------------------------------
  * Paged decode (K1) and the split scheduler (S).
  * ---------------------------------------------------------------------- */

@@ -293,11 +293,22 @@ struct QuantizeParams {
   uint16_t* value_scales;
   int64_t num_pages;
   int heads;
+  int64_t key_token_stride;     // elements between token rows of the source
+  int64_t value_token_stride;
+  // Optional exact ring (prefill): page i is also stored centered in FP16 at
+  // ring page exact_map[i] when exact_map[i] >= 0.
+  const int32_t* exact_map;
+  uint16_t* exact_key;
+  uint16_t* exact_value;
 };
 
-__device__ __forceinline__ void quantize_block(const uint16_t* src, const uint16_t* center,
-                                               int64_t row_stride, int8_t* codes,
-                                               uint16_t* scale_out, int lane) {
+// ``src`` rows are ``src_stride`` elements apart, code rows ``row_stride``.
+// With ``ring`` set, the FP16-rounded centered rows are also written there
+// (row stride ``row_stride``), as the reference's prefill stores exact pages.
+__device__ __forceinline__ void quantize_block(const uint16_t* src, int64_t src_stride,
+                                               const uint16_t* center, int64_t row_stride,
+                                               int8_t* codes, uint16_t* scale_out,
+                                               uint16_t* ring, int lane) {
   const Half2Bits c = load_pair(center + 2 * lane);
   const float c0 = half_bits_to_float(c.lo);
   const float c1 = half_bits_to_float(c.hi);
@@ -306,10 +317,13 @@ __device__ __forceinline__ void quantize_block(const uint16_t* src, const uint16
   float local_max = 0.0f;
 #pragma unroll
   for (int t = 0; t < kPageSize; ++t) {
-    const Half2Bits x = load_pair(src + t * row_stride + 2 * lane);
+    const Half2Bits x = load_pair(src + t * src_stride + 2 * lane);
     lo[t] = half_bits_to_float(x.lo) - c0;
     hi[t] = half_bits_to_float(x.hi) - c1;
     local_max = fmaxf(local_max, fmaxf(fabsf(lo[t]), fabsf(hi[t])));
+    if (ring != nullptr)
+      store_pair(ring + t * row_stride + 2 * lane, __half_as_ushort(__float2half_rn(lo[t])),
+                 __half_as_ushort(__float2half_rn(hi[t])));
   }
   const float maximum = wave_max(local_max);
   const uint16_t scale_bits = stored_scale(maximum);
@@ -333,10 +347,73 @@ __global__ __launch_bounds__(kWave * kWavesPerBlock) void quantize_pages_kernel(
   const int head = static_cast<int>(item % p.heads);
   const int64_t row_stride = static_cast<int64_t>(p.heads) * kHeadDim;
   const int64_t base = (page * kPageSize * p.heads + head) * kHeadDim;
-  quantize_block(p.key + base, p.key_center + head * kHeadDim, row_stride, p.key_codes + base,
-                 p.key_scales + item, lane);
-  quantize_block(p.value + base, p.value_center + head * kHeadDim, row_stride,
-                 p.value_codes + base, p.value_scales + item, lane);
+  const int32_t ring_page = p.exact_map != nullptr ? p.exact_map[page] : -1;
+  const int64_t ring_base = (static_cast<int64_t>(ring_page) * kPageSize * p.heads + head) * kHeadDim;
+  quantize_block(p.key + page * kPageSize * p.key_token_stride + head * kHeadDim,
+                 p.key_token_stride, p.key_center + head * kHeadDim, row_stride,
+                 p.key_codes + base, p.key_scales + item,
+                 ring_page >= 0 ? p.exact_key + ring_base : nullptr, lane);
+  quantize_block(p.value + page * kPageSize * p.value_token_stride + head * kHeadDim,
+                 p.value_token_stride, p.value_center + head * kHeadDim, row_stride,
+                 p.value_codes + base, p.value_scales + item,
+                 ring_page >= 0 ? p.exact_value + ring_base : nullptr, lane);
+}
+
+// Exact per-(head, dim) token mean.  Every FP16 value is an integer multiple
+// of 2^-24, so the column sums are kept exactly as int64 counts of 2^-24 and
+// the result does not depend on the reduction order.  Launch 1 sums the
+// tokens of one chunk per block; launch 2 adds the chunk sums and rounds
+// f16(f32(f64(sum * 2^-24) / tokens)).
+constexpr int kCenterChunk = 64;          // tokens per partial-sum block
+constexpr int kCenterThreads = 256;       // 2 columns per thread -> 512 columns per block
+constexpr int64_t kCenterMaxTokens = int64_t{1} << 22;  // |sum| < 2^40 * 2^22 fits in int64
+
+__device__ __forceinline__ int64_t half_to_fixed24(uint16_t h) {
+  const int e = (h >> 10) & 0x1f;
+  const int64_t m = h & 0x3ff;
+  const int64_t magnitude = e == 0 ? m : ((1024 + m) << (e - 1));
+  return (h & 0x8000u) ? -magnitude : magnitude;
+}
+
+struct CenterParams {
+  const uint16_t* source[2];   // key, value: [tokens, heads, 128] rows
+  int64_t token_stride[2];
+  uint16_t* center[2];         // [heads, 128]
+  int64_t* partial;            // [2][chunks][heads*128]
+  int64_t tokens;
+  int columns;                 // heads * 128
+  int chunks;
+};
+
+__global__ __launch_bounds__(kCenterThreads) void center_partial_kernel(CenterParams p) {
+  const int which = blockIdx.z;
+  const int column = (blockIdx.x * kCenterThreads + threadIdx.x) * 2;
+  if (column >= p.columns) return;
+  const int64_t begin = static_cast<int64_t>(blockIdx.y) * kCenterChunk;
+  const int64_t end = min(begin + kCenterChunk, p.tokens);
+  const uint16_t* src = p.source[which] + column;
+  const int64_t stride = p.token_stride[which];
+  int64_t s0 = 0, s1 = 0;
+#pragma unroll 8
+  for (int64_t t = begin; t < end; ++t) {
+    const Half2Bits x = load_pair(src + t * stride);
+    s0 += half_to_fixed24(x.lo);
+    s1 += half_to_fixed24(x.hi);
+  }
+  int64_t* out = p.partial + (static_cast<int64_t>(which) * p.chunks + blockIdx.y) * p.columns + column;
+  out[0] = s0;
+  out[1] = s1;
+}
+
+__global__ __launch_bounds__(kCenterThreads) void center_finalize_kernel(CenterParams p) {
+  const int which = blockIdx.y;
+  const int column = blockIdx.x * kCenterThreads + threadIdx.x;
+  if (column >= p.columns) return;
+  const int64_t* in = p.partial + static_cast<int64_t>(which) * p.chunks * p.columns + column;
+  int64_t total = 0;
+  for (int c = 0; c < p.chunks; ++c) total += in[static_cast<int64_t>(c) * p.columns];
+  const double mean = (static_cast<double>(total) * 0x1p-24) / static_cast<double>(p.tokens);
+  p.center[which][column] = __half_as_ushort(__float2half_rn(static_cast<float>(mean)));
 }
 
 int32_t check_common(int batch, int query_heads, int kv_heads) {
@@ -358,6 +435,15 @@ int32_t launch_rope_append(UpdateParams p, bool page_gauge, hipStream_t stream) 
                        dim3(kWave * kWavesPerBlock), 0, stream, p);
   }
   return check_launch(page_gauge ? "rope_append_page_gauge" : "rope_append_fp16");
+}
+
+int32_t launch_quantize(const QuantizeParams& p, hipStream_t stream, const char* what) {
+  const int64_t waves = p.num_pages * p.heads;
+  const int64_t blocks = (waves + kWavesPerBlock - 1) / kWavesPerBlock;
+  if (blocks > 0x7fffffff) return fail(PG_ERROR_INVALID_ARGUMENT, "too many pages");
+  hipLaunchKernelGGL(quantize_pages_kernel, dim3(static_cast<unsigned>(blocks)),
+                     dim3(kWave * kWavesPerBlock), 0, stream, p);
+  return check_launch(what);
 }
 
 }  // namespace
@@ -629,10 +715,93 @@ extern "C" int32_t pg_quantize_completed_kv_pages(const void* key, const void* v
   p.value_scales = static_cast<uint16_t*>(value_scales);
   p.num_pages = num_pages;
   p.heads = heads;
-  const int64_t waves = num_pages * heads;
-  const int64_t blocks = (waves + kWavesPerBlock - 1) / kWavesPerBlock;
-  if (blocks > 0x7fffffff) return fail(PG_ERROR_INVALID_ARGUMENT, "too many pages");
-  hipLaunchKernelGGL(quantize_pages_kernel, dim3(static_cast<unsigned>(blocks)),
-                     dim3(kWave * kWavesPerBlock), 0, as_stream(stream), p);
-  return check_launch("quantize_completed_kv_pages");
+  p.key_token_stride = p.value_token_stride = static_cast<int64_t>(heads) * kHeadDim;
+  return launch_quantize(p, as_stream(stream), "quantize_completed_kv_pages");
+}
+
+extern "C" int32_t pg_prefill_page_gauge(const void* key, int64_t key_token_stride,
+                                         const void* value, int64_t value_token_stride,
+                                         const void* key_center, const void* value_center,
+                                         int8_t* key_codes, int8_t* value_codes,
+                                         void* key_scales, void* value_scales,
+                                         const int32_t* exact_page_map, void* exact_key_pages,
+                                         void* exact_value_pages, int64_t num_pages,
+                                         int32_t heads, void* stream) {
+  clear_error();
+  if (num_pages <= 0 || heads <= 0)
+    return fail(PG_ERROR_INVALID_ARGUMENT, "pages and heads must be positive");
+  if (any_null({key, value, key_center, value_center, key_codes, value_codes, key_scales,
+                value_scales}))
+    return fail(PG_ERROR_INVALID_ARGUMENT, "null tensor pointer");
+  if (exact_page_map != nullptr && (exact_key_pages == nullptr || exact_value_pages == nullptr))
+    return fail(PG_ERROR_INVALID_ARGUMENT, "an exact page map needs exact key/value pages");
+  const int64_t row = static_cast<int64_t>(heads) * kHeadDim;
+  if (key_token_stride < row || value_token_stride < row || key_token_stride % 2 ||
+      value_token_stride % 2)
+    return fail(PG_ERROR_INVALID_ARGUMENT,
+                "token strides must be even and cover heads*128 elements");
+  QuantizeParams p{};
+  p.key = static_cast<const uint16_t*>(key);
+  p.value = static_cast<const uint16_t*>(value);
+  p.key_center = static_cast<const uint16_t*>(key_center);
+  p.value_center = static_cast<const uint16_t*>(value_center);
+  p.key_codes = key_codes;
+  p.value_codes = value_codes;
+  p.key_scales = static_cast<uint16_t*>(key_scales);
+  p.value_scales = static_cast<uint16_t*>(value_scales);
+  p.num_pages = num_pages;
+  p.heads = heads;
+  p.key_token_stride = key_token_stride;
+  p.value_token_stride = value_token_stride;
+  p.exact_map = exact_page_map;
+  p.exact_key = static_cast<uint16_t*>(exact_key_pages);
+  p.exact_value = static_cast<uint16_t*>(exact_value_pages);
+  return launch_quantize(p, as_stream(stream), "prefill_page_gauge");
+}
+
+extern "C" int64_t pg_token_major_centers_workspace_bytes(int64_t tokens, int32_t heads) {
+  if (tokens <= 0 || heads <= 0) return 0;
+  const int64_t chunks = (tokens + kCenterChunk - 1) / kCenterChunk;
+  return 2 * chunks * heads * kHeadDim * static_cast<int64_t>(sizeof(int64_t));
+}
+
+extern "C" int32_t pg_token_major_centers(const void* key, int64_t key_token_stride,
+                                          const void* value, int64_t value_token_stride,
+                                          int64_t tokens, int32_t heads, void* key_center,
+                                          void* value_center, void* workspace,
+                                          int64_t workspace_bytes, void* stream) {
+  clear_error();
+  if (tokens <= 0 || heads <= 0)
+    return fail(PG_ERROR_INVALID_ARGUMENT, "token-major K/V must contain tokens and heads");
+  if (tokens > kCenterMaxTokens)
+    return fail(PG_ERROR_INVALID_ARGUMENT, "at most 4194304 tokens per center reduction");
+  if (any_null({key, value, key_center, value_center, workspace}))
+    return fail(PG_ERROR_INVALID_ARGUMENT, "null tensor pointer");
+  const int64_t row = static_cast<int64_t>(heads) * kHeadDim;
+  if (key_token_stride < row || value_token_stride < row || key_token_stride % 2 ||
+      value_token_stride % 2)
+    return fail(PG_ERROR_INVALID_ARGUMENT,
+                "token strides must be even and cover heads*128 elements");
+  if (workspace_bytes < pg_token_major_centers_workspace_bytes(tokens, heads))
+    return fail(PG_ERROR_WORKSPACE, "center workspace too small");
+  CenterParams p{};
+  p.source[0] = static_cast<const uint16_t*>(key);
+  p.source[1] = static_cast<const uint16_t*>(value);
+  p.token_stride[0] = key_token_stride;
+  p.token_stride[1] = value_token_stride;
+  p.center[0] = static_cast<uint16_t*>(key_center);
+  p.center[1] = static_cast<uint16_t*>(value_center);
+  p.partial = static_cast<int64_t*>(workspace);
+  p.tokens = tokens;
+  p.columns = static_cast<int>(row);
+  p.chunks = static_cast<int>((tokens + kCenterChunk - 1) / kCenterChunk);
+  const unsigned column_blocks = static_cast<unsigned>((row / 2 + kCenterThreads - 1) / kCenterThreads);
+  hipLaunchKernelGGL(center_partial_kernel, dim3(column_blocks, p.chunks, 2), dim3(kCenterThreads),
+                     0, as_stream(stream), p);
+  int32_t rc = check_launch("token_major_centers");
+  if (rc != PG_OK) return rc;
+  const unsigned finalize_blocks = static_cast<unsigned>((row + kCenterThreads - 1) / kCenterThreads);
+  hipLaunchKernelGGL(center_finalize_kernel, dim3(finalize_blocks, 2), dim3(kCenterThreads), 0,
+                     as_stream(stream), p);
+  return check_launch("token_major_centers");
 }

@@ -94,3 +94,110 @@ def append_finalize_page_gauge(key, value, key_center, value_center, exact_key_p
                key_scales.data_ptr(), value_scales.data_ptr(), page_ids.data_ptr(),
                page_offsets.data_ptr(), key.shape[0], key.shape[1], exact_key_pages.shape[0],
                _stream())
+
+
+def _token_rows(t: torch.Tensor) -> int:
+    """Token stride (elements) of a [T, H, 128] FP16 tensor whose (H, 128) rows are dense."""
+    if not t.is_cuda or t.dtype != torch.float16:
+        raise ValueError("token-major K/V must be CUDA float16")
+    if t.stride(2) != 1 or t.stride(1) != DIM or t.stride(0) < t.shape[1] * DIM or t.stride(0) % 2:
+        raise ValueError("token-major K/V rows must be dense [heads,128] blocks")
+    return t.stride(0)
+
+
+def token_major_centers(source_key: torch.Tensor, source_value: torch.Tensor,
+                        key_center: torch.Tensor | None = None,
+                        value_center: torch.Tensor | None = None,
+                        workspace: torch.Tensor | None = None):
+    """Per-(head, dim) token means of token-major [T,Hkv,128] K/V, as FP16.
+
+    HIP replacement of ``token_major_centers``
+    (diagnostics/benchmark_backend_exclusive.py:372-395), same shape checks and
+    messages.  The sum is exact (int64 multiples of 2^-24), so the result is
+    f16(f32(exact_sum / T)) whatever the reduction order.  Token rows may be
+    strided (a K or V slice of a fused QKV projection).  Outputs may be given
+    (e.g. ``cache.key_center[layer, request]``); ``workspace`` is a uint8 CUDA
+    tensor of at least ``pg_token_major_centers_workspace_bytes`` bytes.
+    """
+    if source_key.shape != source_value.shape or source_key.ndim != 3:
+        raise ValueError("token-major K/V must have identical [T,Hkv,D] shapes")
+    if source_key.shape[0] <= 0 or source_key.shape[1] <= 0:
+        raise ValueError("token-major K/V must contain tokens and heads")
+    if int(source_key.shape[2]) != DIM:
+        raise ValueError(f"token-major K/V head dimension must be {DIM}")
+    tokens, heads = int(source_key.shape[0]), int(source_key.shape[1])
+    key_stride, value_stride = _token_rows(source_key), _token_rows(source_value)
+    shape = (heads, DIM)
+    if key_center is None:
+        key_center = torch.empty(shape, device=source_key.device, dtype=torch.float16)
+    if value_center is None:
+        value_center = torch.empty(shape, device=source_key.device, dtype=torch.float16)
+    for center in (key_center, value_center):
+        if tuple(center.shape) != shape or center.dtype != torch.float16:
+            raise ValueError(f"centers must be float16 {shape}")
+    _all_cuda_contiguous(key_center, value_center)
+    lib = _capi.library()
+    need = int(lib.pg_token_major_centers_workspace_bytes(tokens, heads))
+    if workspace is None:
+        workspace = torch.empty(need, device=source_key.device, dtype=torch.uint8)
+    if workspace.dtype != torch.uint8 or workspace.numel() < need:
+        raise ValueError(f"center workspace must be a uint8 tensor of at least {need} bytes")
+    _all_cuda_contiguous(workspace)
+    _capi.call("pg_token_major_centers", source_key.data_ptr(), key_stride,
+               source_value.data_ptr(), value_stride, tokens, heads, key_center.data_ptr(),
+               value_center.data_ptr(), workspace.data_ptr(), workspace.numel(), _stream())
+    return key_center, value_center
+
+
+def prefill_page_gauge(source_key: torch.Tensor, source_value: torch.Tensor,
+                       key_center: torch.Tensor, value_center: torch.Tensor,
+                       key_codes: torch.Tensor, value_codes: torch.Tensor,
+                       key_scales: torch.Tensor, value_scales: torch.Tensor,
+                       exact_page_map: torch.Tensor | None = None,
+                       exact_key_pages: torch.Tensor | None = None,
+                       exact_value_pages: torch.Tensor | None = None) -> None:
+    """Quantise a token-major prefix into INT8 pages and store its exact pages.
+
+    Mirrors the cache population of ``populate_backend_cache_layer``
+    (diagnostics/benchmark_backend_exclusive.py:442-506): every page gets
+    codes and scales from float32-centered values (``quantize_completed_kv_pages``
+    arithmetic) and page ``i`` with ``exact_page_map[i] >= 0`` is also written
+    as ``fp16(f32(x) - f32(center))`` into that ring page.  ``source_*`` are
+    [pages*16, Hkv, 128] FP16 (token rows may be strided).
+    """
+    if source_key.shape != source_value.shape or source_key.ndim != 3:
+        raise ValueError("token-major K/V must have identical [T,Hkv,D] shapes")
+    tokens, heads = int(source_key.shape[0]), int(source_key.shape[1])
+    if tokens <= 0 or tokens % PAGE or int(source_key.shape[2]) != DIM:
+        raise ValueError("prefill K/V must be whole 16-token pages of [Hkv,128] rows")
+    pages = tokens // PAGE
+    key_stride, value_stride = _token_rows(source_key), _token_rows(source_value)
+    if key_center.shape != (heads, DIM) or value_center.shape != key_center.shape:
+        raise ValueError("centers must be [heads, 128]")
+    for codes in (key_codes, value_codes):
+        if codes.dtype != torch.int8 or tuple(codes.shape) != (pages, PAGE, heads, DIM):
+            raise ValueError("codes must be int8 [pages,16,heads,128]")
+    for scales in (key_scales, value_scales):
+        if scales.dtype != torch.float16 or tuple(scales.shape) != (pages, heads):
+            raise ValueError("scales must be float16 [pages,heads]")
+    _all_cuda_contiguous(key_center, value_center, key_codes, value_codes, key_scales,
+                         value_scales)
+    map_ptr = ring_k = ring_v = None
+    if exact_page_map is not None:
+        if exact_page_map.dtype != torch.int32 or tuple(exact_page_map.shape) != (pages,):
+            raise ValueError("exact_page_map must be int32 [pages]")
+        if exact_key_pages is None or exact_value_pages is None:
+            raise ValueError("an exact page map needs exact key/value pages")
+        for ring in (exact_key_pages, exact_value_pages):
+            if ring.dtype != torch.float16 or ring.ndim != 4 or tuple(ring.shape[1:]) != (PAGE, heads, DIM):
+                raise ValueError("exact pages must be float16 [ring_pages,16,heads,128]")
+        _all_cuda_contiguous(exact_page_map, exact_key_pages, exact_value_pages)
+        valid = exact_page_map[exact_page_map >= 0]
+        if valid.numel() and int(valid.max()) >= exact_key_pages.shape[0]:
+            raise ValueError("exact_page_map points past the exact pages")
+        map_ptr = exact_page_map.data_ptr()
+        ring_k, ring_v = exact_key_pages.data_ptr(), exact_value_pages.data_ptr()
+    _capi.call("pg_prefill_page_gauge", source_key.data_ptr(), key_stride, source_value.data_ptr(),
+               value_stride, key_center.data_ptr(), value_center.data_ptr(), key_codes.data_ptr(),
+               value_codes.data_ptr(), key_scales.data_ptr(), value_scales.data_ptr(), map_ptr,
+               ring_k, ring_v, pages, heads, _stream())

@@ -1,0 +1,159 @@
+"""The decoder over the PageGauge kernels on the GPU (a reduced Mistral: the
+full 32/8-head, head-dim-128 layout, 2 layers, small MLP and vocabulary).
+
+* PageGauge logits against the same decoder whose attention is the dense
+  float32 softmax over the reconstructed cache (the reference's own path,
+  diagnostics/benchmark_heterogeneous_fa2_correctness.py:291-299);
+* PageGauge against the FP16-cache decoder: the reference's acceptance gate
+  (logit cosine >= 0.995 and top-1 agreement,
+  scripts/benchmark_page_gauge_transformer.py:3865-3903);
+* graph replay bitwise equal to eager steps, a page transition that misses
+  the graph bank and runs eagerly (:3706-3860), and greedy generation."""
+
+from __future__ import annotations
+
+import math
+
+import pytest
+import torch
+import torch.nn.functional as F
+
+pytestmark = pytest.mark.gpu
+
+PROMPT = 512           # 32 pages: 16 INT8 + 16 FP16 tail
+STEPS = 20             # crosses one page boundary (positions 512..531)
+
+
+@pytest.fixture(scope="module")
+def setup(cuda):
+    from pagegauge_amd import decoder as dec
+
+    cfg = dec.DecoderConfig(layers=2, intermediate=512, vocab=1024)
+    weights = dec.DecoderWeights(cfg, seed=20260850, device=cuda)
+    gen = torch.Generator().manual_seed(20260850)
+    prompt = torch.randint(0, cfg.vocab, (PROMPT,), generator=gen)
+    first, logits, decoders = dec.build_decoders(weights, prompt, STEPS + 1)
+    tokens = torch.randint(0, cfg.vocab, (STEPS,), generator=gen).to(cuda)
+    torch.cuda.synchronize()
+    return dec, weights, first, decoders, tokens
+
+
+def _fresh(dec, base, backend=None):
+    """A decoder over a private copy of ``base``'s cache."""
+    cls = type(base) if backend is None else backend
+    d = cls(base.weights, base.cache.clone(), base.backend, base.max_pages * 16, base.rope_cos,
+            base.rope_sin, base.exact_tail_pages * 16, base.split_pages, base.batch_size,
+            base.exact_sink_pages)
+    return d
+
+
+def _dense_reference_class(dec):
+    class DenseReference(dec.PageGaugeDecoder):
+        """Attention = float32 softmax over K = c_K + s*Z (old) / c_K + ring
+        (tail), V likewise, from the same cache the K2 kernel updates."""
+
+        def attention(self, layer):
+            c = self.cache
+            b = 0
+            old = self.old_table.active_indices().long()
+            tail = self.exact_table.active_indices().long()
+            last = int(self.exact_table.host_last_len[b])
+            kc = c.key_center[layer, b].float()
+            vc = c.value_center[layer, b].float()
+            k_old = c.key_codes[layer][old].float() * c.key_scales[layer][old].float()[:, None, :, None]
+            v_old = c.value_codes[layer][old].float() * c.value_scales[layer][old].float()[:, None, :, None]
+            k_tail = c.exact_key[layer][tail].float()
+            v_tail = c.exact_value[layer][tail].float()
+            n_tail = (tail.numel() - 1) * 16 + last
+            keys = torch.cat((k_old.reshape(-1, 8, 128), k_tail.reshape(-1, 8, 128)[:n_tail])) + kc
+            values = torch.cat((v_old.reshape(-1, 8, 128), v_tail.reshape(-1, 8, 128)[:n_tail])) + vc
+            q = self.rotated_query[b].float().view(8, 4, 128)
+            scores = torch.matmul(q, keys.permute(1, 2, 0).contiguous()) / math.sqrt(128)
+            probs = torch.softmax(scores, dim=-1)
+            out = torch.matmul(probs, values.permute(1, 0, 2).contiguous()).reshape(1, 32, 128)
+            self.attention_output[layer].copy_(out.to(torch.float16))
+            return self.attention_output[layer]
+
+    return DenseReference
+
+
+def test_page_gauge_logits_match_dense_reference(setup):
+    dec, weights, first, decoders, tokens = setup
+    pg = _fresh(dec, decoders["page_gauge"])
+    ref = _fresh(dec, decoders["page_gauge"], _dense_reference_class(dec))
+    worst_attn = worst_logit = 0.0
+    for i in range(STEPS):
+        position = PROMPT + i
+        got = pg.step(tokens[i:i + 1], position).clone()
+        attn = pg.attention_output.clone()
+        want = ref.step(tokens[i:i + 1], position)
+        worst_attn = max(worst_attn, float((attn.float() - ref.attention_output.float()).abs().max()))
+        worst_logit = max(worst_logit, float((got - want).abs().max()))
+    print(f"max |attention - dense| = {worst_attn:.3g}, max |logits - dense| = {worst_logit:.3g}")
+    assert worst_attn <= 2e-3
+    assert worst_logit <= 2e-3 * 8     # logits: 2 layers of fp16 GEMMs downstream of attention
+
+
+def test_page_gauge_agrees_with_fp16_cache_decoder(setup):
+    dec, weights, first, decoders, tokens = setup
+    pg = _fresh(dec, decoders["page_gauge"])
+    fp = _fresh(dec, decoders["fp16"])
+    cosines, top1 = [], []
+    for i in range(STEPS):
+        a = pg.step(tokens[i:i + 1], PROMPT + i).clone()
+        b = fp.step(tokens[i:i + 1], PROMPT + i)
+        cosines.append(float(F.cosine_similarity(a, b, dim=-1).min()))
+        top1.append(bool((a.argmax(-1) == b.argmax(-1)).all()))
+    print(f"min cosine {min(cosines):.6f}, top-1 agreement {sum(top1)}/{len(top1)}")
+    assert min(cosines) >= 0.995
+    assert sum(top1) >= 0.8 * len(top1)
+
+
+@pytest.mark.parametrize("backend", ["page_gauge", "fp16"])
+def test_graph_replay_is_bitwise_eager_and_transitions_run_eagerly(setup, backend):
+    dec, weights, first, decoders, tokens = setup
+    eager = _fresh(dec, decoders[backend])
+    graphed = _fresh(dec, decoders[backend])
+    window = 16
+    want = [eager.step(tokens[i:i + 1], PROMPT + i).clone() for i in range(window + 1)]
+    graphed.capture(PROMPT)
+    replays = []
+    for i in range(window):
+        replays.append(graphed.step(tokens[i:i + 1], PROMPT + i).clone())
+        torch.cuda.synchronize()                     # eager host work between replays
+    counts = graphed.counts()
+    assert counts["graph_replays"] == window and counts["eager_steps"] == 0
+    for i in range(window):
+        assert torch.equal(replays[i], want[i]), f"step {i}"
+    # the next token opens a new page: new plan signature, no banked graph
+    transition = graphed.step(tokens[window:window + 1], PROMPT + window)
+    assert graphed.counts()["graph_bank_misses"] == 1
+    assert torch.equal(transition, want[window])
+
+
+def test_greedy_generation_graph_equals_eager(setup):
+    dec, weights, first, decoders, tokens = setup
+    a = _fresh(dec, decoders["page_gauge"])
+    b = _fresh(dec, decoders["page_gauge"])
+    toks_graph, logits_graph = a.generate(first, PROMPT, STEPS, use_graphs=True)
+    toks_eager, logits_eager = b.generate(first, PROMPT, STEPS, use_graphs=False)
+    assert torch.equal(toks_graph, toks_eager)
+    for x, y in zip(logits_graph, logits_eager):
+        assert torch.equal(x, y)
+    assert a.counts()["graph_replays"] == STEPS
+    assert len(a.graph_bank) == 2                     # one per page window
+
+
+def test_decoder_requires_the_hip_library(setup, monkeypatch):
+    from pagegauge_amd import _capi
+
+    from pagegauge_amd import runtime
+
+    dec, weights, first, decoders, tokens = setup
+    monkeypatch.setattr(_capi, "_library", None)
+    monkeypatch.setattr(_capi, "LIBRARY_PATH", _capi.LIBRARY_PATH.with_name("absent.so"))
+    monkeypatch.setattr(runtime, "_EXTENSION", None)
+    with pytest.raises(_capi.LibraryMissingError):
+        _fresh(dec, decoders["page_gauge"])
+    with pytest.raises(_capi.LibraryMissingError):
+        decoders["page_gauge"].step(tokens[:1], PROMPT)     # its first plan needs the library
