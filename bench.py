@@ -321,6 +321,11 @@ def decoder_config5(torch, device, repeats: int, context: int = 16384, steps: in
     torch.cuda.synchronize()
     t1 = time.perf_counter()
     first, _, decoders = dec.build_decoders(weights, prompt, steps + 1)
+    base = decoders["page_gauge"]
+    # the one-launch unified-table variant (a12) over a copy of the same cache
+    decoders["page_gauge_heterogeneous"] = dec.PageGaugeDecoder(
+        weights, base.cache.clone(), "page_gauge", base.max_pages * 16, base.rope_cos,
+        base.rope_sin, tail_attention="heterogeneous")
     torch.cuda.synchronize()
     t2 = time.perf_counter()
     result = {"model": "Mistral-7B architecture, random-init fp16 (32 layers, hidden 4096, "
@@ -332,6 +337,7 @@ def decoder_config5(torch, device, repeats: int, context: int = 16384, steps: in
     kv_bytes["page_gauge"] = cfg.layers * ((per_layer_pages - 16) * (2 * 16 * 8 * 128 + 4 * 8)
                                            + 16 * 2 * 16 * 8 * 256 + 2 * 8 * 128 * 2)
     kv_bytes["fp16"] = cfg.layers * per_layer_pages * 2 * 16 * 8 * 256
+    kv_bytes["page_gauge_heterogeneous"] = kv_bytes["page_gauge"]
     weight_bytes = weights.bytes_per_token()
     logits = {}
     for name, d in decoders.items():

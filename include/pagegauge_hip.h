@@ -183,7 +183,7 @@ typedef struct pg_decode_plan {
   int32_t num_kv_heads;
   int32_t head_dim;
   int32_t page_size;
-  int32_t primary_kind;   /* PG_KV_INT8 or PG_KV_FP16: element type of segment 0 */
+  int32_t primary_kind;   /* PG_KV_INT8, PG_KV_FP16 or PG_KV_HETEROGENEOUS (segment 0) */
   int32_t has_tail;       /* 1 if an FP16 tail segment joins the softmax */
   int32_t split_pages;    /* pages per work item, segment 0 */
   int32_t tail_split_pages;
@@ -196,7 +196,12 @@ typedef struct pg_decode_plan {
   int64_t workspace_bytes;
 } pg_decode_plan_t;
 
-enum { PG_KV_INT8 = 0, PG_KV_FP16 = 1 };
+/* PG_KV_HETEROGENEOUS: one unified page table per request whose first
+ * old_kv_len[r] / 16 entries index INT8 code pages and the rest FP16 exact
+ * pages; old_kv_len is a device array read by every run
+ * (pg_decode_run_heterogeneous), so the boundary may move without re-planning.
+ * Work items are 48 bytes. */
+enum { PG_KV_INT8 = 0, PG_KV_FP16 = 1, PG_KV_HETEROGENEOUS = 2 };
 
 /* Bytes of workspace a plan with these bounds needs: total work items over
  * the batch, and the largest number of work items of one request. */
@@ -259,9 +264,9 @@ int32_t pg_decode_plan_host(const int32_t* host_indptr, const int32_t* host_last
  * out fp16 [B,Hq,128] and, if lse != NULL, base-2 lse [B,Hq].
  * Replaces the patched FlashInfer run (int8 patch, prefill.cuh), FlashInfer's
  * split merge, the tail decode, merge_state_in_place and add_(output_center)
- * of scripts/benchmark_flashinfer_page_affine_int8.py:566-602, or the
- * heterogeneous one-launch run (scripts/page_gauge_heterogeneous_fa2.py:355-381).
- * GQA group size must be 4 and head_dim 128. */
+ * of scripts/benchmark_flashinfer_page_affine_int8.py:566-602.  GQA group
+ * size must be 4 and head_dim 128.  Unused rows of an FP16 last page may hold
+ * anything (NaN included): they never reach the output. */
 int32_t pg_decode_run(const pg_decode_plan_t* plan, const void* query,
                       int64_t query_batch_stride, const void* k_cache, const void* v_cache,
                       const void* k_scale, const void* v_scale, const int32_t* indices,
@@ -269,6 +274,24 @@ int32_t pg_decode_run(const pg_decode_plan_t* plan, const void* query,
                       const int32_t* tail_indices, const int32_t* tail_last_len,
                       const void* value_center, int64_t center_batch_stride, void* out,
                       float* lse, float sm_scale, void* workspace, void* stream);
+
+/* Run a PG_KV_HETEROGENEOUS plan: replaces the heterogeneous one-launch run
+ * (scripts/page_gauge_heterogeneous_fa2.py:336-381, kernel
+ * patches/flashinfer-0.6.17-page-gauge-heterogeneous-fa2.patch).  Entry j of
+ * request r's table (indices[indptr[r] + j]) indexes k_codes/v_codes (with
+ * k_scale/v_scale) when j < old_kv_len[r] / 16 and exact_k/exact_v (FP16
+ * centered pages) otherwise; old_kv_len (device int32 [B], page aligned) and
+ * last_page_len are read at run time.  value_center [B,Hkv,128] (stride
+ * center_batch_stride) is added once.  Same partial + combine launches and
+ * outputs as pg_decode_run. */
+int32_t pg_decode_run_heterogeneous(const pg_decode_plan_t* plan, const void* query,
+                                    int64_t query_batch_stride, const void* k_codes,
+                                    const void* v_codes, const void* k_scale, const void* v_scale,
+                                    const void* exact_k, const void* exact_v,
+                                    const int32_t* indices, const int32_t* last_page_len,
+                                    const int32_t* old_kv_len, const void* value_center,
+                                    int64_t center_batch_stride, void* out, float* lse,
+                                    float sm_scale, void* workspace, void* stream);
 
 /* The two launches of pg_decode_run, for callers that schedule them
  * separately (e.g. to time the partial kernel, or to overlap the combine
@@ -340,6 +363,33 @@ int32_t pg_exact_tail_merge_center(const void* query, const void* exact_key_page
                                    int64_t center_batch_stride, int32_t batch_size,
                                    int32_t query_heads, int32_t kv_heads,
                                    int32_t pages_per_request, float sm_scale, void* stream);
+
+/* ------------------------------------------------------------------------
+ * Decoder step (the caller of the path): fused projections.
+ * ------------------------------------------------------------------------ */
+
+/* out = epilogue(W @ prologue(x)) for a decode batch of 1-4 rows.
+ * Replaces the F.linear calls of the decoder layer and the element-wise work
+ * around them (scripts/benchmark_page_gauge_transformer.py:2754-2805:
+ * MistralRMSNorm before the QKV and gate/up projections, SiLU(gate)*up after
+ * the gate/up projection, the two residual adds, the final norm + LM head).
+ *   weight [n, k] fp16 row-major, k a multiple of 512;
+ *   x [batch, x_stride] fp16 (x_stride a multiple of 8); with norm_weight [k]
+ *     the input is fp16(w * fp16(x * rsqrt(mean(x^2) + eps)));
+ *   swiglu != 0: n is even, rows [0, n/2) are the gate and [n/2, n) the up
+ *     projection, and out[i] = fp16(fp16(silu(y[i])) * y[i + n/2]) for
+ *     i < n/2 (out has n/2 columns);
+ *   residual [batch, residual_stride] fp16 or NULL (may alias out): the
+ *     projection is rounded to fp16 first, then added in fp16;
+ *   out [batch, out_stride] fp16, or float32 when out_f32 != 0 (the fp16
+ *     result widened, as `linear(...).float()`).
+ * k = 4096 and k = 14336 run the blocked kernel (weights prefetched before
+ * the input prologue); other k stage the input in LDS (batch * k <= 32768).
+ * Float32 accumulation with v_dot2_f32_f16; every weight byte is read once. */
+int32_t pg_decoder_gemv(const void* weight, int32_t n, int32_t k, const void* x,
+                        int64_t x_stride, int32_t batch, const void* norm_weight, float eps,
+                        int32_t swiglu, const void* residual, int64_t residual_stride, void* out,
+                        int64_t out_stride, int32_t out_f32, void* stream);
 
 #ifdef __cplusplus
 }

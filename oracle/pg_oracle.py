@@ -50,6 +50,10 @@ PINNED = {
     "decode": "torch float64 softmax attention; logsumexp identity; merge associativity",
     "merge_state": "decode(A u B) == merge(decode(A), decode(B))",
     "exact_tail_merge_center": "torch oracle of tests/test_page_gauge_append_extension.py:628-657",
+    "exact_center": "exact-rational (Fraction) mean rounded f64 -> f32 -> f16",
+    "decode_heterogeneous": "dense float64 softmax over the logical sequence (old pages "
+    "reconstructed, then exact pages) of diagnostics/benchmark_heterogeneous_fa2_correctness.py:"
+    "291-299 on its nine boundary CASES (:63-73)",
 }
 
 
@@ -445,6 +449,35 @@ def decode(query, k_pages, v_pages, indptr, indices, last_page_len, sm_scale: fl
         outs[request] = o
         lses[request] = lse
     return outs.astype(np.float16), lses.astype(np.float32), outs
+
+
+def decode_heterogeneous(query, k_codes, v_codes, k_scale, v_scale, exact_k, exact_v, indptr,
+                         indices, last_page_len, old_kv_len, sm_scale: float, value_center=None):
+    """One unified table per request (scripts/page_gauge_heterogeneous_fa2.py:336-381):
+    entry j of request r indexes the INT8 code pool when j < old_kv_len[r]/16
+    and the FP16 exact pages otherwise; the last entry holds last_page_len[r]
+    tokens.  Restated as the segmented decode above (INT8 pages then the FP16
+    pages of each request in one softmax)."""
+    indptr = np.asarray(indptr, dtype=np.int64)
+    indices = np.asarray(indices, dtype=np.int64)
+    batch = indptr.shape[0] - 1
+    old_ptr, tail_ptr = [0], [0]
+    old_idx, tail_idx, old_last, tail_last = [], [], [], []
+    for r in range(batch):
+        row = indices[indptr[r]:indptr[r + 1]]
+        n_old = min(int(old_kv_len[r]) // PAGE, row.shape[0])
+        old_idx.extend(row[:n_old])
+        tail_idx.extend(row[n_old:])
+        old_ptr.append(len(old_idx))
+        tail_ptr.append(len(tail_idx))
+        has_tail = row.shape[0] > n_old
+        old_last.append(PAGE if has_tail else int(last_page_len[r]))
+        tail_last.append(int(last_page_len[r]))
+    return decode(query, k_codes, v_codes, np.array(old_ptr), np.array(old_idx, dtype=np.int64),
+                  np.array(old_last), sm_scale, k_scale=k_scale, v_scale=v_scale, tail_k=exact_k,
+                  tail_v=exact_v, tail_indptr=np.array(tail_ptr),
+                  tail_indices=np.array(tail_idx, dtype=np.int64),
+                  tail_last_page_len=np.array(tail_last), value_center=value_center)
 
 
 def exact_tail_merge_center(query, exact_key_pages, exact_value_pages, exact_page_indices,

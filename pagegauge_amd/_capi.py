@@ -17,6 +17,7 @@ ABI_VERSION = 1
 PG_OK = 0
 PG_KV_INT8 = 0
 PG_KV_FP16 = 1
+PG_KV_HETEROGENEOUS = 2
 
 _p = ctypes.c_void_p
 _i32 = ctypes.c_int32
@@ -81,7 +82,11 @@ PROTOTYPES = {
                                      _p, _p, _p, _p, _f32, _p, _p]),
     "pg_decode_run_partial_timed": (_i32, [ctypes.POINTER(DecodePlan), _p, _i64, _p, _p, _p, _p,
                                            _p, _p, _p, _p, _p, _p, _f32, _p, _p, _p, _p]),
+    "pg_decode_run_heterogeneous": (_i32, [ctypes.POINTER(DecodePlan), _p, _i64, _p, _p, _p, _p,
+                                           _p, _p, _p, _p, _p, _p, _i64, _p, _p, _f32, _p, _p]),
     "pg_decode_run_combine": (_i32, [ctypes.POINTER(DecodePlan), _p, _i64, _p, _p, _p, _p]),
+    "pg_decoder_gemv": (_i32, [_p, _i32, _i32, _p, _i64, _i32, _p, _f32, _i32, _p, _i64, _p, _i64,
+                               _i32, _p]),
     "pg_merge_state_in_place": (_i32, [_p, _p, _p, _p, _p, _i32, _i32, _i32, _p]),
     "pg_exact_tail_merge_center": (_i32, [_p, _p, _p, _p, _p, _p, _p, _p, _i64, _i32, _i32, _i32,
                                           _i32, _f32, _p]),

@@ -37,6 +37,7 @@ SOURCES = {
     "pg_error.cpp": [],
     "pg_update.hip": ["-ffp-contract=off"],
     "pg_decode.hip": [],
+    "pg_decoder.hip": [],
 }
 
 

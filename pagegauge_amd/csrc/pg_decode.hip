@@ -73,8 +73,10 @@ struct WorkItem {
   int32_t last_page;   // absolute index of the segment's final page for the request
   int32_t item_in_request;  // position of this item among its request's items
   int32_t items_in_request; // number of items of the request
+  int32_t request_page_begin;  // absolute index of the request's first page in the segment
+  int32_t reserved[3];
 };
-static_assert(sizeof(WorkItem) == 32, "work item layout");
+static_assert(sizeof(WorkItem) == 48, "work item layout");
 
 struct DecodeArgs {
   const uint16_t* query;
@@ -89,6 +91,7 @@ struct DecodeArgs {
   const uint16_t* tail_v;
   const int32_t* tail_indices;
   const int32_t* tail_last_len;
+  const int32_t* old_kv_len;   // heterogeneous plans: INT8 tokens per request (page aligned)
   const WorkItem* items;
   float* partial_o;   // [items][Hq][128]
   float* partial_m;   // [items][Hq]
@@ -508,6 +511,13 @@ __device__ __forceinline__ void fp16_pages(const DecodeArgs& a, int request, con
 #pragma unroll
     for (int j = 0; j < 4; ++j) acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(qa[j], cur.k[j], acc, 0, 0, 0);
     const int lim = slot == last_slot ? last_len : kPageSize;
+    if (lim < kPageSize) {
+      // rows past the last token: zero V so that p = 0 cannot meet a NaN or
+      // Inf left in unused ring rows
+#pragma unroll
+      for (int k = 0; k < 4; ++k)
+        if (4 * kg + k >= lim) cur.v[k] = v4u{0u, 0u, 0u, 0u};
+    }
     const float score = acc.x * a.sm_scale_log2;
     float s[1] = {m16 < lim ? score : kNegInf};
     float p[1];
@@ -717,6 +727,23 @@ __global__ __launch_bounds__(kWave * kMaxWavesPerBlock) void decode_partial_kern
       int8_chunk<8 * kHeadDim>(a, it, kv, lane, lds, st);
     else
       int8_chunk<0>(a, it, kv, lane, lds, st);
+  } else if (it.kind == PG_KV_HETEROGENEOUS) {
+    // One unified table: the request's first old_kv_len/16 pages are INT8
+    // codes, the rest index the FP16 exact pages.  The boundary is read at run
+    // time; an item that straddles it runs both paths into one state.
+    const int boundary = min(max(it.request_page_begin + a.old_kv_len[it.request] / kPageSize,
+                                 it.page_begin), it.page_end);
+    if (boundary > it.page_begin) {
+      WorkItem old_part = it;
+      old_part.page_end = boundary;
+      if (a.num_kv_heads == 8)
+        int8_chunk<8 * kHeadDim>(a, old_part, kv, lane, lds, st);
+      else
+        int8_chunk<0>(a, old_part, kv, lane, lds, st);
+    }
+    if (boundary < it.page_end)
+      fp16_pages(a, it.request, a.tail_k, a.tail_v, a.indices, boundary, it.page_end, it.last_page,
+                 a.last_page_len[it.request], kv, lane, lds, st);
   } else if (it.segment == 0) {
     fp16_pages(a, it.request, static_cast<const uint16_t*>(a.k_cache),
                static_cast<const uint16_t*>(a.v_cache), a.indices, it.page_begin, it.page_end,
@@ -875,8 +902,11 @@ int32_t build_plan(const int32_t* host_indptr, const int32_t* host_last_page_len
   if (num_kv_heads <= 0 || num_qo_heads != kGqa * num_kv_heads)
     return fail(PG_ERROR_UNSUPPORTED, "the decode kernel requires GQA group size 4");
   if (num_kv_heads > 64) return fail(PG_ERROR_UNSUPPORTED, "at most 64 KV heads");
-  if (primary_kind != PG_KV_INT8 && primary_kind != PG_KV_FP16)
-    return fail(PG_ERROR_INVALID_ARGUMENT, "kv kind must be INT8 or FP16");
+  if (primary_kind != PG_KV_INT8 && primary_kind != PG_KV_FP16 &&
+      primary_kind != PG_KV_HETEROGENEOUS)
+    return fail(PG_ERROR_INVALID_ARGUMENT, "kv kind must be INT8, FP16 or heterogeneous");
+  if (primary_kind == PG_KV_HETEROGENEOUS && host_tail_indptr != nullptr)
+    return fail(PG_ERROR_INVALID_ARGUMENT, "a heterogeneous plan has one unified page table");
   if ((host_tail_indptr == nullptr) != (host_tail_last_len == nullptr))
     return fail(PG_ERROR_INVALID_ARGUMENT, "tail indptr and last_page_len go together");
 
@@ -971,7 +1001,8 @@ int32_t build_plan(const int32_t* host_indptr, const int32_t* host_last_page_len
       for (int k = 0; k < c; ++k) {
         const int size = n / c + (k < n % c ? 1 : 0);
         items.push_back(WorkItem{b, sg.kind, sg.seg, start, start + size, sg.end - 1,
-                                 static_cast<int32_t>(items.size()) - item_ptr[b], 0});
+                                 static_cast<int32_t>(items.size()) - item_ptr[b], 0, sg.begin,
+                                 {0, 0, 0}});
         start += size;
         if (sg.seg == 0) split_pages = std::max(split_pages, size);
         else tail_split_pages = std::max(tail_split_pages, size);
@@ -1107,14 +1138,20 @@ int32_t launch_partial(const pg_decode_plan_t* plan, const void* query,
                        const void* k_scale, const void* v_scale, const int32_t* indices,
                        const int32_t* last_page_len, const void* tail_k, const void* tail_v,
                        const int32_t* tail_indices, const int32_t* tail_last_len, float sm_scale,
-                       void* workspace, void* stream, void* start_event, void* stop_event) {
+                       void* workspace, void* stream, void* start_event, void* stop_event,
+                       const int32_t* old_kv_len = nullptr) {
   clear_error();
   if (!plan || !query || !workspace) return fail(PG_ERROR_INVALID_ARGUMENT, "null run argument");
+  if ((plan->primary_kind == PG_KV_HETEROGENEOUS) != (old_kv_len != nullptr))
+    return fail(PG_ERROR_INVALID_ARGUMENT,
+                "old_kv_len goes with (and only with) a heterogeneous plan");
   if (plan->num_items_primary > 0) {
     if (!k_cache || !v_cache || !indices || !last_page_len)
       return fail(PG_ERROR_INVALID_ARGUMENT, "primary segment tensors missing");
-    if (plan->primary_kind == PG_KV_INT8 && (!k_scale || !v_scale))
+    if (plan->primary_kind != PG_KV_FP16 && (!k_scale || !v_scale))
       return fail(PG_ERROR_INVALID_ARGUMENT, "INT8 pages need k_scale and v_scale");
+    if (plan->primary_kind == PG_KV_HETEROGENEOUS && (!tail_k || !tail_v))
+      return fail(PG_ERROR_INVALID_ARGUMENT, "heterogeneous pages need the exact K/V pages");
   }
   if (plan->num_items > plan->num_items_primary &&
       (!tail_k || !tail_v || !tail_indices || !tail_last_len))
@@ -1137,6 +1174,7 @@ int32_t launch_partial(const pg_decode_plan_t* plan, const void* query,
   a.tail_v = static_cast<const uint16_t*>(tail_v);
   a.tail_indices = tail_indices;
   a.tail_last_len = tail_last_len;
+  a.old_kv_len = old_kv_len;
   a.items = reinterpret_cast<const WorkItem*>(ws + plan->items_offset);
   a.partial_o = pv.o;
   a.partial_m = pv.m;
@@ -1193,10 +1231,12 @@ int32_t run_decode(const pg_decode_plan_t* plan, const void* query, int64_t quer
                    const void* tail_k, const void* tail_v, const int32_t* tail_indices,
                    const int32_t* tail_last_len, const void* value_center,
                    int64_t center_batch_stride, void* out, float* lse, float sm_scale,
-                   void* workspace, void* stream, void* start_event, void* stop_event) {
+                   void* workspace, void* stream, void* start_event, void* stop_event,
+                   const int32_t* old_kv_len = nullptr) {
   if (int32_t rc = launch_partial(plan, query, query_batch_stride, k_cache, v_cache, k_scale,
                                   v_scale, indices, last_page_len, tail_k, tail_v, tail_indices,
-                                  tail_last_len, sm_scale, workspace, stream, start_event, nullptr))
+                                  tail_last_len, sm_scale, workspace, stream, start_event, nullptr,
+                                  old_kv_len))
     return rc;
   return launch_combine(plan, value_center, center_batch_stride, out, lse, workspace, stream,
                         stop_event);
@@ -1262,6 +1302,21 @@ extern "C" int32_t pg_decode_run_timed(const pg_decode_plan_t* plan, const void*
                     last_page_len, tail_k, tail_v, tail_indices, tail_last_len, value_center,
                     center_batch_stride, out, lse, sm_scale, workspace, stream, start_event,
                     stop_event);
+}
+
+extern "C" int32_t pg_decode_run_heterogeneous(
+    const pg_decode_plan_t* plan, const void* query, int64_t query_batch_stride,
+    const void* k_codes, const void* v_codes, const void* k_scale, const void* v_scale,
+    const void* exact_k, const void* exact_v, const int32_t* indices,
+    const int32_t* last_page_len, const int32_t* old_kv_len, const void* value_center,
+    int64_t center_batch_stride, void* out, float* lse, float sm_scale, void* workspace,
+    void* stream) {
+  clear_error();
+  if (!old_kv_len) return fail(PG_ERROR_INVALID_ARGUMENT, "old_kv_len is required");
+  return run_decode(plan, query, query_batch_stride, k_codes, v_codes, k_scale, v_scale, indices,
+                    last_page_len, exact_k, exact_v, nullptr, nullptr, value_center,
+                    center_batch_stride, out, lse, sm_scale, workspace, stream, nullptr, nullptr,
+                    old_kv_len);
 }
 
 extern "C" int32_t pg_merge_state_in_place(void* v, float* s, const void* v_other,

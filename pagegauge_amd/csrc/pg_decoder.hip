@@ -1,0 +1,408 @@
+// Decoder-step projections for gfx950: y = W x with the neighbouring
+// element-wise work fused in, for batch-1..4 decode steps.
+//
+// One launch replaces, per projection of a Mistral decoder layer
+// (scripts/benchmark_page_gauge_transformer.py:2754-2805):
+//   * MistralRMSNorm of the input (float32 mean of squares, rsqrt, FP16
+//     product with the norm weight) -- prologue;
+//   * F.linear with FP16 weights and float32 accumulation;
+//   * SiLU(gate) * up of the fused gate/up projection -- epilogue: the
+//     workgroup that computes gate row i also computes up row i + n/2;
+//   * the residual add (FP16 output of the projection, then an FP16 add) --
+//     epilogue.
+//
+// The work is HBM-bound weight streaming (M = batch <= 4): every weight byte
+// is read once.  A workgroup (4 waves) owns a group of rows; the 512-element
+// chunks of a row are split over its waves (kC consecutive chunks each), a
+// lane reads 16 bytes of every chunk (a wave covers 1 KiB per load
+// instruction, fully coalesced), and every weight load of the group is issued
+// before anything else, the input included.  Each wave then loads only its
+// own slice of the input into registers; the RMSNorm needs one cross-wave sum
+// of squares through LDS.  Products use v_dot2_f32_f16; the wave sums meet in
+// LDS and one lane per output row applies the epilogue.
+#include "pg_common.h"
+
+namespace pg {
+namespace {
+
+typedef _Float16 v8h_t __attribute__((ext_vector_type(8)));
+typedef uint32_t v4u_t __attribute__((ext_vector_type(4)));
+
+constexpr int kGemvThreads = 256;
+constexpr int kGemvWaves = kGemvThreads / kWave;
+constexpr int kChunk = 512;          // elements per wave-wide 16-byte load
+constexpr int kUnroll = 4;           // chunks in flight per row (generic kernel)
+constexpr int kMaxBatch = 4;
+constexpr int kMaxBlocks = 2048;
+constexpr size_t kMaxStagedBytes = 64 * 1024;   // generic kernel: input staged in LDS
+// Output rows per workgroup of the blocked kernels (k = 4096 with n <= 8192
+// or larger; k = 14336).  A SwiGLU workgroup loads twice as many rows.
+#ifndef PG_GEMV_ROWS_4096
+#define PG_GEMV_ROWS_4096 2
+#endif
+#ifndef PG_GEMV_ROWS_4096_LARGE
+#define PG_GEMV_ROWS_4096_LARGE 4
+#endif
+#ifndef PG_GEMV_ROWS_14336
+#define PG_GEMV_ROWS_14336 2
+#endif
+
+struct GemvArgs {
+  const uint16_t* weight;      // [n, k] row-major FP16
+  const uint16_t* x;           // [batch, x_stride]
+  int64_t x_stride;
+  const uint16_t* norm_weight; // [k] or null
+  float eps;
+  int swiglu;                  // out[i] = silu(y[i]) * y[i + n/2], i < n/2
+  const uint16_t* residual;    // [batch, residual_stride] or null; may alias out
+  int64_t residual_stride;
+  void* out;                   // [batch, out_stride] FP16 (or float32 if out_f32)
+  int64_t out_stride;
+  int out_f32;
+  int n;                       // weight rows
+  int out_rows;                // n, or n/2 with swiglu
+  int k;
+  int iterations;
+};
+
+__device__ __forceinline__ float h2f(uint16_t b) { return half_bits_to_float(b); }
+__device__ __forceinline__ uint16_t f2h(float f) { return __half_as_ushort(__float2half_rn(f)); }
+
+// Eight FP16 products summed into a float32 accumulator (4 x v_dot2_f32_f16).
+// The halves are taken from a whole-vector bit cast: bit-casting a single
+// element of an ext_vector (w[e]) miscompiles on this clang (element 0 is
+// used for every e).
+__device__ __forceinline__ float dot8(v4u_t w, v4u_t x, float acc) {
+  const v8h_t wh = __builtin_bit_cast(v8h_t, w);
+  const v8h_t xh = __builtin_bit_cast(v8h_t, x);
+  acc = __builtin_amdgcn_fdot2(__builtin_shufflevector(wh, wh, 0, 1),
+                               __builtin_shufflevector(xh, xh, 0, 1), acc, false);
+  acc = __builtin_amdgcn_fdot2(__builtin_shufflevector(wh, wh, 2, 3),
+                               __builtin_shufflevector(xh, xh, 2, 3), acc, false);
+  acc = __builtin_amdgcn_fdot2(__builtin_shufflevector(wh, wh, 4, 5),
+                               __builtin_shufflevector(xh, xh, 4, 5), acc, false);
+  acc = __builtin_amdgcn_fdot2(__builtin_shufflevector(wh, wh, 6, 7),
+                               __builtin_shufflevector(xh, xh, 6, 7), acc, false);
+  return acc;
+}
+
+// Sum of squares of 8 FP16 values in float32.
+__device__ __forceinline__ float squares8(v4u_t x) {
+  const v8h_t h = __builtin_bit_cast(v8h_t, x);
+  float s = 0.0f;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    const float f = static_cast<float>(h[e]);
+    s += f * f;
+  }
+  return s;
+}
+
+// MistralRMSNorm of 8 values: fp16(w * fp16(x * inv)).
+__device__ __forceinline__ v4u_t normalize8(v4u_t x, v4u_t w, float inv) {
+  const v8h_t xh = __builtin_bit_cast(v8h_t, x);
+  const v8h_t wh = __builtin_bit_cast(v8h_t, w);
+  v8h_t r;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    const float n = static_cast<float>(static_cast<_Float16>(static_cast<float>(xh[e]) * inv));
+    r[e] = static_cast<_Float16>(static_cast<float>(wh[e]) * n);
+  }
+  return __builtin_bit_cast(v4u_t, r);
+}
+
+// torch: F.silu(gate) (float32 math, FP16 result) * up (an FP16 product).
+__device__ __forceinline__ float swiglu(float gate, float up) {
+  const float act = h2f(f2h(gate / (1.0f + expf(-gate))));
+  return h2f(f2h(act * up));
+}
+
+// Writes one output element: FP16 projection value (or the SwiGLU of two),
+// plus the residual in FP16, widened to float32 if requested.
+__device__ __forceinline__ void store_output(const GemvArgs& a, int b, int row, float y0, float y1) {
+  float y = h2f(f2h(y0));
+  if (a.swiglu) y = swiglu(y, h2f(f2h(y1)));
+  if (a.residual != nullptr) y = h2f(f2h(h2f(a.residual[b * a.residual_stride + row]) + y));
+  if (a.out_f32)
+    static_cast<float*>(a.out)[b * a.out_stride + row] = y;
+  else
+    static_cast<uint16_t*>(a.out)[b * a.out_stride + row] = f2h(y);
+}
+
+// Weight row of the block's r-th loaded row: output rows row0.. (and, with
+// SwiGLU, the matching up rows n/2 + row0..); rows past the end are clamped
+// (loaded, never stored).
+template <int kR>
+__device__ __forceinline__ int loaded_row(const GemvArgs& a, int row0, int r) {
+  const int out_row = min(row0 + (r % kR), a.out_rows - 1);
+  return r < kR ? out_row : out_row + a.out_rows;
+}
+
+template <int kR, int kLoad, int kC>
+__device__ __forceinline__ void load_rows(const GemvArgs& a, int row0, int wave, int lane,
+                                          v4u_t (&wr)[kLoad][kC]) {
+#pragma unroll
+  for (int r = 0; r < kLoad; ++r) {
+    const int row = loaded_row<kR>(a, row0, r);
+    const uint16_t* w = a.weight + static_cast<int64_t>(row) * a.k + (wave * kC) * kChunk + lane * 8;
+#pragma unroll
+    for (int c = 0; c < kC; ++c)
+      wr[r][c] = __builtin_nontemporal_load(reinterpret_cast<const v4u_t*>(w + c * kChunk));
+  }
+}
+
+// Blocked kernel: k = 4 * kC * 512.  kR output rows per workgroup (2*kR
+// weight rows with SwiGLU); grid-stride over row groups when the grid is
+// capped.
+template <int kBatch, int kR, int kC, bool kSwiglu>
+__global__ __launch_bounds__(kGemvThreads) void decoder_gemv_kernel(GemvArgs a) {
+  constexpr int kLoad = kSwiglu ? 2 * kR : kR;
+  __shared__ float partial[kGemvWaves][kBatch][kLoad];
+  __shared__ float squares[kGemvWaves][kBatch];
+  const int wave = threadIdx.x / kWave;
+  const int lane = threadIdx.x % kWave;
+  v4u_t wr[kLoad][kC];
+  int row0 = blockIdx.x * kR;
+  if (row0 < a.out_rows) load_rows<kR, kLoad, kC>(a, row0, wave, lane, wr);
+
+  // this wave's slice of the input, in registers
+  v4u_t xv[kBatch][kC];
+#pragma unroll
+  for (int b = 0; b < kBatch; ++b) {
+#pragma unroll
+    for (int c = 0; c < kC; ++c)
+      xv[b][c] = *reinterpret_cast<const v4u_t*>(a.x + b * a.x_stride + (wave * kC + c) * kChunk +
+                                                lane * 8);
+  }
+  if (a.norm_weight != nullptr) {
+#pragma unroll
+    for (int b = 0; b < kBatch; ++b) {
+      float ss = 0.0f;
+#pragma unroll
+      for (int c = 0; c < kC; ++c) ss += squares8(xv[b][c]);
+      ss = wave_sum(ss);
+      if (lane == 0) squares[wave][b] = ss;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int b = 0; b < kBatch; ++b) {
+      float total = 0.0f;
+#pragma unroll
+      for (int w = 0; w < kGemvWaves; ++w) total += squares[w][b];
+      const float inv = rsqrtf(total / static_cast<float>(a.k) + a.eps);
+#pragma unroll
+      for (int c = 0; c < kC; ++c) {
+        const v4u_t g = *reinterpret_cast<const v4u_t*>(a.norm_weight + (wave * kC + c) * kChunk +
+                                                       lane * 8);
+        xv[b][c] = normalize8(xv[b][c], g, inv);
+      }
+    }
+  }
+
+  for (int it = 0; it < a.iterations; ++it, row0 += gridDim.x * kR) {
+    if (row0 >= a.out_rows) break;                         // uniform over the block
+    if (it > 0) load_rows<kR, kLoad, kC>(a, row0, wave, lane, wr);
+    float acc[kBatch][kLoad];
+#pragma unroll
+    for (int b = 0; b < kBatch; ++b) {
+#pragma unroll
+      for (int r = 0; r < kLoad; ++r) acc[b][r] = 0.0f;
+    }
+#pragma unroll
+    for (int c = 0; c < kC; ++c) {
+#pragma unroll
+      for (int b = 0; b < kBatch; ++b) {
+#pragma unroll
+        for (int r = 0; r < kLoad; ++r) acc[b][r] = dot8(wr[r][c], xv[b][c], acc[b][r]);
+      }
+    }
+#pragma unroll
+    for (int b = 0; b < kBatch; ++b) {
+#pragma unroll
+      for (int r = 0; r < kLoad; ++r) {
+        const float total = wave_sum(acc[b][r]);
+        if (lane == 0) partial[wave][b][r] = total;
+      }
+    }
+    __syncthreads();
+    if (threadIdx.x < kBatch * kR) {
+      const int b = threadIdx.x / kR;
+      const int r = threadIdx.x % kR;
+      const int row = row0 + r;
+      if (row < a.out_rows) {
+        float y0 = 0.0f, y1 = 0.0f;
+#pragma unroll
+        for (int w = 0; w < kGemvWaves; ++w) {
+          y0 += partial[w][b][r];
+          if (kSwiglu) y1 += partial[w][b][kR + r];
+        }
+        store_output(a, b, row, y0, y1);
+      }
+    }
+    __syncthreads();                               // partial[] is reused next iteration
+  }
+}
+
+// Any k (a multiple of 512): the input staged in LDS (with the RMSNorm
+// applied), one wave per output row pair (loaded rows i, i+1) or, with
+// SwiGLU, per output row (loaded rows i and i + n/2), chunks streamed four
+// at a time.
+template <int kBatch>
+__global__ __launch_bounds__(kGemvThreads) void decoder_gemv_generic_kernel(GemvArgs a) {
+  extern __shared__ __attribute__((aligned(16))) uint16_t xs[];   // [kBatch][k]
+  __shared__ float squares[kGemvWaves];
+  const int k = a.k;
+  for (int b = 0; b < kBatch; ++b) {
+    const uint16_t* src = a.x + b * a.x_stride;
+    uint16_t* dst = xs + b * k;
+    float ss = 0.0f;
+    for (int i = threadIdx.x * 8; i < k; i += kGemvThreads * 8) {
+      const v4u_t v = *reinterpret_cast<const v4u_t*>(src + i);
+      ss += squares8(v);
+      *reinterpret_cast<v4u_t*>(dst + i) = v;
+    }
+    if (a.norm_weight != nullptr) {
+      ss = wave_sum(ss);
+      __syncthreads();
+      if (threadIdx.x % kWave == 0) squares[threadIdx.x / kWave] = ss;
+      __syncthreads();
+      float total = 0.0f;
+      for (int w = 0; w < kGemvWaves; ++w) total += squares[w];
+      const float inv = rsqrtf(total / static_cast<float>(k) + a.eps);
+      for (int i = threadIdx.x * 8; i < k; i += kGemvThreads * 8) {
+        const v4u_t g = *reinterpret_cast<const v4u_t*>(a.norm_weight + i);
+        *reinterpret_cast<v4u_t*>(dst + i) = normalize8(*reinterpret_cast<v4u_t*>(dst + i), g, inv);
+      }
+    }
+  }
+  __syncthreads();
+  const int wave = threadIdx.x / kWave;
+  const int lane = threadIdx.x % kWave;
+  const int chunks = k / kChunk;
+  const int per_wave = a.swiglu ? 1 : 2;           // output rows per wave
+  for (int it = 0; it < a.iterations; ++it) {
+    const int row0 = ((it * gridDim.x + blockIdx.x) * kGemvWaves + wave) * per_wave;
+    if (row0 >= a.out_rows) break;
+    const int second = a.swiglu ? row0 + a.out_rows : min(row0 + 1, a.out_rows - 1);
+    const uint16_t* w0 = a.weight + static_cast<int64_t>(row0) * k + lane * 8;
+    const uint16_t* w1 = a.weight + static_cast<int64_t>(second) * k + lane * 8;
+    float acc[kBatch][2];
+#pragma unroll
+    for (int b = 0; b < kBatch; ++b) acc[b][0] = acc[b][1] = 0.0f;
+    for (int j = 0; j < chunks; j += kUnroll) {
+      v4u_t wr[kUnroll][2];
+#pragma unroll
+      for (int u = 0; u < kUnroll; ++u) {
+        if (j + u < chunks) {
+          wr[u][0] = __builtin_nontemporal_load(reinterpret_cast<const v4u_t*>(w0 + (j + u) * kChunk));
+          wr[u][1] = __builtin_nontemporal_load(reinterpret_cast<const v4u_t*>(w1 + (j + u) * kChunk));
+        }
+      }
+#pragma unroll
+      for (int u = 0; u < kUnroll; ++u) {
+        if (j + u < chunks) {
+#pragma unroll
+          for (int b = 0; b < kBatch; ++b) {
+            const v4u_t xv = *reinterpret_cast<const v4u_t*>(xs + b * k + (j + u) * kChunk + lane * 8);
+            acc[b][0] = dot8(wr[u][0], xv, acc[b][0]);
+            acc[b][1] = dot8(wr[u][1], xv, acc[b][1]);
+          }
+        }
+      }
+    }
+#pragma unroll
+    for (int b = 0; b < kBatch; ++b) {
+      const float y0 = wave_sum(acc[b][0]);
+      const float y1 = wave_sum(acc[b][1]);
+      if (lane == 0) {
+        if (a.swiglu) {
+          store_output(a, b, row0, y0, y1);
+        } else {
+          store_output(a, b, row0, y0, 0.0f);
+          if (row0 + 1 < a.out_rows) store_output(a, b, row0 + 1, y1, 0.0f);
+        }
+      }
+    }
+  }
+}
+
+template <int kBatch>
+int32_t launch_gemv(GemvArgs a, hipStream_t s) {
+  const int chunks = a.k / kChunk;
+  auto blocked = [&](auto kernel, int rows) {
+    int64_t blocks = (static_cast<int64_t>(a.out_rows) + rows - 1) / rows;
+    a.iterations = static_cast<int>((blocks + kMaxBlocks - 1) / kMaxBlocks);
+    blocks = (blocks + a.iterations - 1) / a.iterations;
+    hipLaunchKernelGGL(kernel, dim3(static_cast<unsigned>(blocks)), dim3(kGemvThreads), 0, s, a);
+  };
+  if (chunks == 8 && !a.swiglu) {                 // k = 4096
+    if (a.out_rows > 8192)
+      blocked(decoder_gemv_kernel<kBatch, PG_GEMV_ROWS_4096_LARGE, 2, false>, PG_GEMV_ROWS_4096_LARGE);
+    else
+      blocked(decoder_gemv_kernel<kBatch, PG_GEMV_ROWS_4096, 2, false>, PG_GEMV_ROWS_4096);
+  } else if (chunks == 8) {
+    blocked(decoder_gemv_kernel<kBatch, PG_GEMV_ROWS_4096, 2, true>, PG_GEMV_ROWS_4096);
+  } else if (chunks == 28 && !a.swiglu) {         // k = 14336
+    blocked(decoder_gemv_kernel<kBatch, PG_GEMV_ROWS_14336, 7, false>, PG_GEMV_ROWS_14336);
+  } else {
+    const size_t lds = static_cast<size_t>(kBatch) * a.k * sizeof(uint16_t);
+    if (lds > kMaxStagedBytes)
+      return fail(PG_ERROR_UNSUPPORTED, "batch * input width exceeds the 32768-element LDS staging");
+    const int per_wave = a.swiglu ? 1 : 2;
+    const int64_t waves = (static_cast<int64_t>(a.out_rows) + per_wave - 1) / per_wave;
+    int64_t blocks = (waves + kGemvWaves - 1) / kGemvWaves;
+    a.iterations = static_cast<int>((blocks + kMaxBlocks - 1) / kMaxBlocks);
+    blocks = (waves + static_cast<int64_t>(kGemvWaves) * a.iterations - 1) /
+             (static_cast<int64_t>(kGemvWaves) * a.iterations);
+    hipLaunchKernelGGL(decoder_gemv_generic_kernel<kBatch>, dim3(static_cast<unsigned>(blocks)),
+                       dim3(kGemvThreads), lds, s, a);
+  }
+  return check_launch("decoder_gemv");
+}
+
+}  // namespace
+}  // namespace pg
+
+using namespace pg;
+
+extern "C" int32_t pg_decoder_gemv(const void* weight, int32_t n, int32_t k, const void* x,
+                                   int64_t x_stride, int32_t batch, const void* norm_weight,
+                                   float eps, int32_t swiglu, const void* residual,
+                                   int64_t residual_stride, void* out, int64_t out_stride,
+                                   int32_t out_f32, void* stream) {
+  clear_error();
+  if (weight == nullptr || x == nullptr || out == nullptr)
+    return fail(PG_ERROR_INVALID_ARGUMENT, "null tensor pointer");
+  if (n <= 0 || k <= 0 || k % kChunk)
+    return fail(PG_ERROR_INVALID_ARGUMENT, "rows must be positive and the input width a multiple of 512");
+  if (batch < 1 || batch > kMaxBatch)
+    return fail(PG_ERROR_UNSUPPORTED, "decoder projections take a batch of 1 to 4 rows");
+  if (swiglu && n % 2)
+    return fail(PG_ERROR_INVALID_ARGUMENT, "a SwiGLU projection needs gate and up rows (even n)");
+  const int out_rows = swiglu ? n / 2 : n;
+  if (x_stride < k || x_stride % 8 || (residual != nullptr && residual_stride < out_rows) ||
+      out_stride < out_rows)
+    return fail(PG_ERROR_INVALID_ARGUMENT, "row strides must cover the rows (input stride a multiple of 8)");
+  GemvArgs a{};
+  a.weight = static_cast<const uint16_t*>(weight);
+  a.x = static_cast<const uint16_t*>(x);
+  a.x_stride = x_stride;
+  a.norm_weight = static_cast<const uint16_t*>(norm_weight);
+  a.eps = eps;
+  a.swiglu = swiglu;
+  a.residual = static_cast<const uint16_t*>(residual);
+  a.residual_stride = residual_stride;
+  a.out = out;
+  a.out_stride = out_stride;
+  a.out_f32 = out_f32;
+  a.n = n;
+  a.out_rows = out_rows;
+  a.k = k;
+  hipStream_t s = as_stream(stream);
+  switch (batch) {
+    case 1: return launch_gemv<1>(a, s);
+    case 2: return launch_gemv<2>(a, s);
+    case 3: return launch_gemv<3>(a, s);
+    default: return launch_gemv<4>(a, s);
+  }
+}

@@ -115,7 +115,8 @@ class _Planned:
 
 
 WORK_ITEM_FIELDS = ("request", "kind", "segment", "page_begin", "page_end", "last_page",
-                    "item_in_request", "items_in_request")
+                    "item_in_request", "items_in_request", "request_page_begin", "reserved0",
+                    "reserved1", "reserved2")
 
 
 def plan_work_items(indptr, last_page_len, tail_indptr=None, tail_last_page_len=None,
@@ -126,7 +127,7 @@ def plan_work_items(indptr, last_page_len, tail_indptr=None, tail_last_page_len=
 
     Returns ``(plan, items, item_ptr)``: the ``DecodePlan`` that
     ``pg_decode_plan`` would produce, the work list as an int32 tensor
-    [num_items, 8] with columns ``WORK_ITEM_FIELDS``, and [B+1] per-request
+    [num_items, 12] with columns ``WORK_ITEM_FIELDS``, and [B+1] per-request
     item offsets.  Same validation and error messages as ``plan``.
     """
     lib = _capi.library()
@@ -135,7 +136,8 @@ def plan_work_items(indptr, last_page_len, tail_indptr=None, tail_last_page_len=
     host_tail = None if tail_indptr is None else _host_i32(tail_indptr)
     host_tail_last = None if tail_last_page_len is None else _host_i32(tail_last_page_len)
     batch = host_indptr.numel() - 1
-    kind = _capi.PG_KV_INT8 if kv_data_type == torch.int8 else _capi.PG_KV_FP16
+    kind = {torch.int8: _capi.PG_KV_INT8, torch.float16: _capi.PG_KV_FP16,
+            "heterogeneous": _capi.PG_KV_HETEROGENEOUS}[kv_data_type]
     plan = _capi.DecodePlan()
     args = (host_indptr.data_ptr(), host_last.data_ptr(), batch, kind,
             None if host_tail is None else host_tail.data_ptr(),
@@ -433,6 +435,137 @@ class PageGaugeSegmentedDecode:
                    self._tail[0].data_ptr(), self._tail[1].data_ptr(), float(scale))
         combine = (_ptr(value_center), center_stride, out.data_ptr(), _ptr(lse))
         return BoundDecode(self._state, partial, combine, _stream() if stream is None else stream)
+
+
+def validate_heterogeneous_run_inputs(query, old_k_cache, old_v_cache, k_page_scale, v_page_scale,
+                                      exact_k_cache, exact_v_cache, old_kv_len,
+                                      value_center) -> None:
+    """The reference's ABI checks (scripts/page_gauge_heterogeneous_fa2.py:286-333),
+    same messages.  The page-alignment check reads ``old_kv_len`` on the host."""
+    batch = int(query.shape[0]) if query.ndim == 3 else -1
+    if tuple(query.shape) != (batch, HQ, DIM) or query.dtype != torch.float16:
+        raise ValueError(f"query must have decode-only shape [B,{HQ},{DIM}] and dtype float16")
+    if query.device.type != "cuda" or not query.is_contiguous():
+        raise ValueError("query must be contiguous CUDA storage")
+    for name, cache, dtype in (("old_k_cache", old_k_cache, torch.int8),
+                               ("old_v_cache", old_v_cache, torch.int8),
+                               ("exact_k_cache", exact_k_cache, torch.float16),
+                               ("exact_v_cache", exact_v_cache, torch.float16)):
+        if (cache.device.type != "cuda" or cache.dtype != dtype or cache.ndim != 4
+                or tuple(cache.shape[1:]) != (PAGE, HKV, DIM) or not cache.is_contiguous()):
+            raise ValueError(f"{name} must be contiguous CUDA [{name.split('_')[0]}_pages,16,8,128] "
+                             f"{dtype}")
+    if old_k_cache.shape != old_v_cache.shape or exact_k_cache.shape != exact_v_cache.shape:
+        raise ValueError("K/V cache shapes must match within each representation")
+    for name, scale in (("k_page_scale", k_page_scale), ("v_page_scale", v_page_scale)):
+        if (scale.device.type != "cuda" or scale.dtype != torch.float16
+                or tuple(scale.shape) != (old_k_cache.shape[0], HKV) or not scale.is_contiguous()):
+            raise ValueError(f"{name} must be contiguous CUDA [old_pages,{HKV}] float16")
+    if (old_kv_len.device.type != "cuda" or old_kv_len.dtype != torch.int32
+            or tuple(old_kv_len.shape) != (batch,) or not old_kv_len.is_contiguous()):
+        raise ValueError("old_kv_len must be contiguous CUDA [B] int32")
+    if bool(torch.any(old_kv_len % PAGE).item()):
+        raise ValueError(f"old_kv_len must be page-aligned ({PAGE} tokens)")
+    if (value_center.device.type != "cuda" or value_center.dtype != torch.float16
+            or tuple(value_center.shape) != (batch, HKV, DIM) or not value_center.is_contiguous()):
+        raise ValueError(f"value_center must be contiguous CUDA [B,{HKV},{DIM}] float16")
+
+
+class HeterogeneousDecodeWrapper:
+    """One-launch decode over a unified page table (INT8 history pages then
+    FP16 exact pages per request): ``make_heterogeneous_page_gauge_wrapper``
+    of scripts/page_gauge_heterogeneous_fa2.py:159-205 with its ``plan`` /
+    ``run`` contract (:240-283, :336-381).
+
+    ``plan(indptr, indices, last_page_len, 32, 8, 128, 16, ...)`` cuts the
+    unified table into work items without knowing the INT8/FP16 boundary;
+    ``run(q, (old_k, old_v), k_page_scale, v_page_scale, exact_k, exact_v,
+    old_kv_len, value_center, sm_scale, out=, lse=)`` reads ``old_kv_len``
+    (page aligned, device int32 [B]) on the GPU, so a caller may move the
+    boundary in place between runs.  Entries below the boundary index the
+    code pool, the others the exact FP16 pages.
+    """
+
+    def __init__(self, float_workspace_buffer: torch.Tensor, kv_layout: str = "NHD",
+                 use_cuda_graph: bool = False, **_unused) -> None:
+        if kv_layout != "NHD":
+            raise ValueError("only the NHD layout is supported")
+        self._state = _Planned(float_workspace_buffer)
+        self.use_cuda_graph = use_cuda_graph
+
+    def plan(self, indptr, indices, last_page_len, num_qo_heads: int = HQ,
+             num_kv_heads: int = HKV, head_dim: int = DIM, page_size: int = PAGE,
+             pos_encoding_mode: str = "NONE", q_data_type=torch.float16,
+             kv_data_type=torch.int8, o_data_type=torch.float16, sm_scale=None,
+             fixed_split_size: Optional[int] = None, num_cus: Optional[int] = None,
+             **_unused) -> None:
+        if pos_encoding_mode != "NONE":
+            raise ValueError("only pos_encoding_mode='NONE' is supported")
+        if kv_data_type != torch.int8 or q_data_type != torch.float16 or o_data_type != torch.float16:
+            raise ValueError("the heterogeneous decode takes fp16 queries/outputs over int8 history")
+        _check_index(indices, "indices")
+        _check_index(last_page_len, "last_page_len")
+        host_indptr = _host_i32(indptr)
+        self._state.make_plan(host_indptr, _host_i32(last_page_len), _capi.PG_KV_HETEROGENEOUS,
+                              None, None, num_qo_heads, num_kv_heads, head_dim, page_size,
+                              fixed_split_size or 0, 0, indices.device, num_cus)
+        self._indices = indices
+        self._last_page_len = last_page_len
+        self._batch = host_indptr.numel() - 1
+        self._num_qo_heads = num_qo_heads
+        self._num_kv_heads = num_kv_heads
+        self._sm_scale = sm_scale if sm_scale is not None else 1.0 / math.sqrt(head_dim)
+
+    @property
+    def split_pages(self) -> int:
+        return self._state.split_pages
+
+    @property
+    def num_work_items(self) -> int:
+        return self._state.num_items
+
+    def run(self, q, paged_kv_cache, k_page_scale, v_page_scale, exact_k_cache, exact_v_cache,
+            old_kv_len, value_center, sm_scale: Optional[float] = None, out=None, lse=None,
+            return_lse: bool = False, **_unused):
+        if not self._state.planned:
+            raise RuntimeError("plan() must be called before run()")
+        old_k, old_v = paged_kv_cache
+        _check_query(q, self._batch, self._num_qo_heads)
+        _check_cache(old_k, "old_k_cache", torch.int8, self._num_kv_heads)
+        _check_cache(old_v, "old_v_cache", torch.int8, self._num_kv_heads)
+        _check_scale(k_page_scale, "k_page_scale", old_k.size(0), self._num_kv_heads)
+        _check_scale(v_page_scale, "v_page_scale", old_v.size(0), self._num_kv_heads)
+        _check_cache(exact_k_cache, "exact_k_cache", torch.float16, self._num_kv_heads)
+        _check_cache(exact_v_cache, "exact_v_cache", torch.float16, self._num_kv_heads)
+        _check_index(old_kv_len, "old_kv_len")
+        if old_kv_len.numel() != self._batch:
+            raise ValueError("old_kv_len must be contiguous CUDA [B] int32")
+        if (value_center.dtype != torch.float16 or not value_center.is_contiguous()
+                or tuple(value_center.shape) != (self._batch, self._num_kv_heads, DIM)):
+            raise ValueError("value_center must be contiguous CUDA [B,Hkv,128] float16")
+        if out is None:
+            out = torch.empty_like(q)
+        if return_lse and lse is None:
+            lse = torch.empty(q.size(0), q.size(1), device=q.device, dtype=torch.float32)
+        scale = self._sm_scale if sm_scale is None else float(sm_scale)
+        _capi.call("pg_decode_run_heterogeneous", ctypes.byref(self._state.plan), q.data_ptr(),
+                   q.stride(0), old_k.data_ptr(), old_v.data_ptr(), k_page_scale.data_ptr(),
+                   v_page_scale.data_ptr(), exact_k_cache.data_ptr(), exact_v_cache.data_ptr(),
+                   self._indices.data_ptr(), self._last_page_len.data_ptr(), old_kv_len.data_ptr(),
+                   value_center.data_ptr(), self._num_kv_heads * DIM, out.data_ptr(), _ptr(lse),
+                   scale, self._state.workspace.data_ptr(), _stream())
+        return (out, lse) if return_lse else out
+
+
+def make_heterogeneous_page_gauge_wrapper(flashinfer_module, workspace: torch.Tensor,
+                                          **wrapper_kwargs) -> HeterogeneousDecodeWrapper:
+    """scripts/page_gauge_heterogeneous_fa2.py:159-205; the first argument (the
+    flashinfer module in the reference) is ignored."""
+    if not workspace.is_cuda or workspace.dtype != torch.uint8:
+        raise ValueError("workspace must be a CUDA uint8 tensor")
+    wrapper = HeterogeneousDecodeWrapper(workspace, "NHD", **wrapper_kwargs)
+    wrapper.page_gauge_module_uri = "pagegauge_amd/libpagegauge_hip.so:heterogeneous"
+    return wrapper
 
 
 def merge_state_in_place(v: torch.Tensor, s: torch.Tensor, v_other: torch.Tensor,

@@ -38,7 +38,8 @@ import torch
 import torch.nn.functional as F
 
 from . import page_table as pt
-from .decode import BatchDecodeWithPagedKVCacheWrapper, PageGaugeSegmentedDecode
+from .decode import (BatchDecodeWithPagedKVCacheWrapper, HeterogeneousDecodeWrapper,
+                     PageGaugeSegmentedDecode)
 from .runtime import load_append_extension
 from .update import prefill_page_gauge, token_major_centers
 
@@ -115,6 +116,42 @@ class DecoderWeights:
         """Weight bytes streamed by one decode step (embedding row excluded)."""
         per_layer = sum(w.numel() * w.element_size() for w in self.layers[0].values())
         return self.config.layers * per_layer + self.lm_head.numel() * 2 + self.norm.numel() * 2
+
+
+def projection(weight: torch.Tensor, x: torch.Tensor, out: torch.Tensor, *,
+               norm_weight: Optional[torch.Tensor] = None, eps: float = 1.0e-5,
+               swiglu: bool = False, residual: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """``out = epilogue(weight @ prologue(x))`` in one HIP launch
+    (``pg_decoder_gemv``).  Prologue: MistralRMSNorm with ``norm_weight``, or
+    nothing.  Epilogue: the projection rounded to FP16; with ``swiglu`` the
+    weight rows are [gate; up] and ``out[i] = silu(gate_i) * up_i`` (FP16
+    ops, ``out`` has N/2 columns); then ``residual`` added in FP16
+    (``residual`` may be ``out``).  ``out`` is FP16 or float32 [B, N']."""
+    from . import _capi
+
+    n, k = int(weight.shape[0]), int(weight.shape[1])
+    batch = int(x.shape[0])
+    if weight.dtype != torch.float16 or not weight.is_contiguous() or x.dtype != torch.float16:
+        raise ValueError("projection weights and inputs must be FP16 (weights contiguous)")
+    if x.dim() != 2 or x.stride(1) != 1 or x.shape[1] != k:
+        raise ValueError("projection input must be [B, K] rows")
+    width = n // 2 if swiglu else n
+    if out.dim() != 2 or tuple(out.shape) != (batch, width) or out.stride(1) != 1:
+        raise ValueError("projection output must be [B, N] rows ([B, N/2] with SwiGLU)")
+    if residual is not None and (tuple(residual.shape) != (batch, width) or residual.stride(1) != 1
+                                 or residual.dtype != torch.float16):
+        raise ValueError("residual must be FP16 rows shaped like the output")
+    if norm_weight is not None and (norm_weight.numel() != k or norm_weight.dtype != torch.float16):
+        raise ValueError("norm weight must be FP16 [K]")
+    out_f32 = out.dtype == torch.float32
+    if not out_f32 and out.dtype != torch.float16:
+        raise ValueError("projection output must be FP16 or float32")
+    _capi.call("pg_decoder_gemv", weight.data_ptr(), n, k, x.data_ptr(), x.stride(0), batch,
+               None if norm_weight is None else norm_weight.data_ptr(), float(eps), int(swiglu),
+               None if residual is None else residual.data_ptr(),
+               0 if residual is None else residual.stride(0), out.data_ptr(), out.stride(0),
+               int(out_f32), torch.cuda.current_stream().cuda_stream)
+    return out
 
 
 def rms_norm(x: torch.Tensor, weight: torch.Tensor, eps: float) -> torch.Tensor:
@@ -366,9 +403,15 @@ class PageGaugeDecoder:
     def __init__(self, weights: DecoderWeights, cache, backend: str, max_context: int,
                  rope_cos: torch.Tensor, rope_sin: torch.Tensor, exact_tail: int = 256,
                  split_pages: int = 0, batch_size: int = 1, exact_sink_pages: int = 0,
-                 workspace_bytes: int = 128 * 1024 * 1024) -> None:
+                 workspace_bytes: int = 128 * 1024 * 1024, fused: Optional[bool] = None,
+                 tail_attention: str = "segmented") -> None:
         if backend not in ("page_gauge", "fp16"):
             raise ValueError(f"unknown backend {backend}")
+        if tail_attention not in ("segmented", "heterogeneous"):
+            raise ValueError(f"unknown exact-tail attention path {tail_attention}")
+        if tail_attention == "heterogeneous" and exact_sink_pages:
+            raise ValueError("exact prefix pages require the segmented flashinfer_merge path")
+        self.tail_attention = tail_attention
         if batch_size <= 0:
             raise ValueError("batch size must be positive")
         if exact_tail <= 0 or exact_tail % PAGE:
@@ -407,10 +450,20 @@ class PageGaugeDecoder:
             self.exact_plan_pages = torch.empty(
                 batch_size, self.exact_tail_pages + self.exact_sink_pages, device=device,
                 dtype=torch.int32)
-            self.old_table = SegmentTable(batch_size, self.max_pages, device)
-            self.exact_table = SegmentTable(batch_size, self.exact_tail_pages + self.exact_sink_pages,
-                                            device)
-            self.decode = PageGaugeSegmentedDecode(self.workspace)
+            if tail_attention == "heterogeneous":
+                # one unified table: INT8 code pages, then the exact ring
+                # (scripts/benchmark_page_gauge_transformer.py:1817-1830, :2085-2110)
+                self.heterogeneous_pages = torch.empty_like(self.all_pages)
+                self.old_kv_len = torch.zeros(batch_size, device=device, dtype=torch.int32)
+                self.heterogeneous_layout: Optional[tuple] = None
+                self.heterogeneous_page_table_updates = 0
+                self.table = SegmentTable(batch_size, self.max_pages, device)
+                self.decode = HeterogeneousDecodeWrapper(self.workspace)
+            else:
+                self.old_table = SegmentTable(batch_size, self.max_pages, device)
+                self.exact_table = SegmentTable(batch_size,
+                                                self.exact_tail_pages + self.exact_sink_pages, device)
+                self.decode = PageGaugeSegmentedDecode(self.workspace)
         else:
             if not isinstance(cache, Fp16Cache) or cache.pages_per_request != self.max_pages:
                 raise ValueError("baseline cache must use request-major [L,B*P,16,Hkv,D] storage")
@@ -438,6 +491,20 @@ class PageGaugeDecoder:
         self.graph_replays = 0
         self.eager_steps = 0
         self.graph_bank_misses = 0
+        # fused projections (pg_decoder_gemv): batch <= 4, widths multiples of
+        # 512, and batch * width <= 32768 unless the width is 4096 or 14336
+        ok = batch_size <= 4 and all(
+            w % 512 == 0 and (w in (4096, 14336) or batch_size * w <= 32768)
+            for w in (cfg.hidden, cfg.intermediate))
+        self.fused = ok if fused is None else fused
+        if self.fused and not ok:
+            raise ValueError("fused projections need batch <= 4 and widths that are multiples "
+                             "of 512 (4096 / 14336, or batch * width <= 32768)")
+        self._hidden = torch.empty(batch_size, cfg.hidden, device=device, dtype=torch.float16)
+        self._qkv = torch.empty(batch_size, cfg.qkv_width, device=device, dtype=torch.float16)
+        self._activation = torch.empty(batch_size, cfg.intermediate, device=device,
+                                       dtype=torch.float16)
+        self._logits = torch.empty(batch_size, cfg.vocab, device=device, dtype=torch.float32)
 
     # -- plan --------------------------------------------------------------
     def plan(self, context: int) -> None:
@@ -467,6 +534,22 @@ class PageGaugeDecoder:
         self.exact_pages = int(partition["exact_page_count"])
         old_tokens = int(partition["old_token_count"])
         exact_tokens = int(partition["exact_token_count"])
+        if self.tail_attention == "heterogeneous":
+            layout = (self.old_pages, pages)
+            if layout != self.heterogeneous_layout:
+                pt.write_heterogeneous_page_table(self.heterogeneous_pages, self.all_pages,
+                                                  self.exact_ring_pages, self.old_pages, pages)
+                self.old_kv_len.fill_(old_tokens)
+                self.heterogeneous_layout = layout
+                self.heterogeneous_page_table_updates += 1
+            if self.table.plan(self.heterogeneous_pages[:, :pages], context, last_len,
+                               self.split_pages, page_table_epoch=self.heterogeneous_page_table_updates):
+                self.decode.plan(self.table.host_indptr, self.table.active_indices(),
+                                 self.table.last_len, self.config.q_heads, self.config.kv_heads,
+                                 DIM, PAGE, fixed_split_size=self.split_pages or None)
+                self.kernel_replans += 1
+            self.plan_signature_value = ("heterogeneous", self.table.signature)
+            return
         old_begin = partition["old_logical_pages"][0]
         old_indices = self.all_pages[:, old_begin:old_begin + self.old_pages]
         changed = self.old_table.plan(old_indices, old_tokens, PAGE, self.split_pages)
@@ -520,10 +603,31 @@ class PageGaugeDecoder:
                                                         self.cache.value[layer]), out=out)
         c = self.cache
         value_center = c.value_center[layer]
+        if self.tail_attention == "heterogeneous":
+            return self.decode.run(self.rotated_query, (c.key_codes[layer], c.value_codes[layer]),
+                                   c.key_scales[layer], c.value_scales[layer], c.exact_key[layer],
+                                   c.exact_value[layer], self.old_kv_len, value_center, out=out)
         return self.decode.run(self.rotated_query, (c.key_codes[layer], c.value_codes[layer]),
                                c.key_scales[layer], c.value_scales[layer],
                                (c.exact_key[layer], c.exact_value[layer]),
                                value_center=value_center, out=out)
+
+    def _layer_fused(self, layer: int) -> None:
+        """One layer on ``self._hidden`` in place: 4 projection launches + K2 + K1."""
+        cfg = self.config
+        w = self.weights.layers[layer]
+        b = self.batch_size
+        qkv = projection(w["qkv"], self._hidden, self._qkv, norm_weight=w["input_norm"],
+                         eps=cfg.rms_eps)
+        qw, kw = cfg.q_heads * DIM, cfg.kv_heads * DIM
+        self._append(layer, qkv[:, :qw].view(b, cfg.q_heads, DIM),
+                     qkv[:, qw:qw + kw].view(b, cfg.kv_heads, DIM),
+                     qkv[:, qw + kw:].view(b, cfg.kv_heads, DIM))
+        attended = self.attention(layer)
+        projection(w["o"], attended.view(b, qw), self._hidden, residual=self._hidden)
+        projection(w["gate_up"], self._hidden, self._activation, norm_weight=w["post_norm"],
+                   eps=cfg.rms_eps, swiglu=True)
+        projection(w["down"], self._activation, self._hidden, residual=self._hidden)
 
     def _layer(self, layer: int, hidden: torch.Tensor) -> torch.Tensor:
         cfg = self.config
@@ -543,6 +647,13 @@ class PageGaugeDecoder:
         return hidden + F.linear(F.silu(gate) * up, w["down"])
 
     def _body(self, token: torch.Tensor) -> torch.Tensor:
+        if self.fused:
+            torch.index_select(self.weights.embed, 0, token.reshape(self.batch_size),
+                               out=self._hidden)
+            for layer in range(self.config.layers):
+                self._layer_fused(layer)
+            return projection(self.weights.lm_head, self._hidden, self._logits,
+                              norm_weight=self.weights.norm, eps=self.config.rms_eps)
         hidden = F.embedding(token.reshape(self.batch_size), self.weights.embed)
         for layer in range(self.config.layers):
             hidden = self._layer(layer, hidden)
@@ -615,11 +726,10 @@ class PageGaugeDecoder:
             logits = self.step(token, position)
             if use_graphs and self.plan_signature() in self.graph_bank:
                 token = self.graph_next.clone()
-                logits = logits.clone()
             else:
                 token = logits.argmax(dim=-1)
             tokens.append(token)
-            logits_seq.append(logits)
+            logits_seq.append(logits.clone())
         return torch.stack(tokens), logits_seq
 
     def plan_signature_after(self, position: int) -> Optional[tuple]:
@@ -632,7 +742,7 @@ class PageGaugeDecoder:
                "graph_replays": self.graph_replays, "eager_steps": self.eager_steps,
                "graph_bank_misses": self.graph_bank_misses,
                "exact_page_table_updates": self.exact_page_table_updates}
-        if self.backend == "fp16":
+        if self.backend == "fp16" or self.tail_attention == "heterogeneous":
             out["table"] = self.table.operation_counts()
         else:
             out["old_table"] = self.old_table.operation_counts()

@@ -69,10 +69,10 @@ def test_plan_struct_layout_matches_header():
 
 def test_workspace_bytes_closed_form():
     lib = _capi.library()
-    # items (32 B each) + item_ptr + partials (B * Hq * items * (128 + 2) floats), 256-aligned
+    # items (48 B each) + item_ptr + partials (B * Hq * items * (128 + 2) floats), 256-aligned
     got = lib.pg_decode_workspace_bytes(1, 32, 193, 193)
     align = lambda x: (x + 255) // 256 * 256  # noqa: E731
-    assert got == align(193 * 32) + align(2 * 4) + align(32 * 193 * 130 * 4)
+    assert got == align(193 * 48) + align(2 * 4) + align(32 * 193 * 130 * 4)
     assert lib.pg_decode_workspace_bytes(0, 32, 1, 1) == 0
 
 

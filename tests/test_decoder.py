@@ -71,6 +71,7 @@ class _FakeSegmented:
 def _plan_only_decoder(batch, max_pages, tail_pages, sink_pages):
     d = dec.PageGaugeDecoder.__new__(dec.PageGaugeDecoder)
     d.backend = "page_gauge"
+    d.tail_attention = "segmented"
     d.config = dec.DecoderConfig(layers=1, intermediate=8, vocab=8)
     d.decoder_plan_calls = d.kernel_replans = d.exact_page_table_updates = 0
     d.max_pages, d.batch_size = max_pages, batch
@@ -243,3 +244,35 @@ def test_decoder_config_rejects_unsupported_head_layouts():
         dec.DecoderConfig(hidden=4096, q_heads=32, kv_heads=4)
     with pytest.raises(ValueError, match="head_dim 128"):
         dec.DecoderConfig(hidden=4000)
+
+
+class _FakeUnified:
+    def __init__(self):
+        self.calls = []
+
+    def plan(self, indptr, indices, last, *args, **kwargs):
+        self.calls.append((indptr.tolist(), indices.tolist(), last.tolist()))
+
+
+def test_heterogeneous_decoder_plan_writes_one_unified_table():
+    # reference :2085-2110 and tests/test_page_gauge_transformer.py:199-216
+    d = _plan_only_decoder(batch=2, max_pages=8, tail_pages=2, sink_pages=0)
+    d.tail_attention = "heterogeneous"
+    d.heterogeneous_pages = torch.empty_like(d.all_pages)
+    d.old_kv_len = torch.zeros(2, dtype=torch.int32)
+    d.heterogeneous_layout = None
+    d.heterogeneous_page_table_updates = 0
+    d.table = dec.SegmentTable(2, 8, "cpu")
+    d.decode = _FakeUnified()
+    d.plan(8 * PAGE)
+    indptr, indices, last = d.decode.calls[-1]
+    assert indptr == [0, 8, 16]
+    assert indices == [0, 1, 2, 3, 4, 5, 0, 1, 8, 9, 10, 11, 12, 13, 2, 3]
+    assert last == [16, 16] and d.old_kv_len.tolist() == [96, 96]
+    d.plan(8 * PAGE - 3)                     # same layout: no new table, no new plan
+    assert d.heterogeneous_page_table_updates == 1 and d.kernel_replans == 1
+    assert d.table.last_len.tolist() == [13, 13]
+    d.plan(7 * PAGE)                         # one page less: new layout
+    assert d.heterogeneous_page_table_updates == 2 and d.kernel_replans == 2
+    assert d.decode.calls[-1][1] == [0, 1, 2, 3, 4, 1, 0, 8, 9, 10, 11, 12, 3, 2]
+    assert d.old_kv_len.tolist() == [80, 80]

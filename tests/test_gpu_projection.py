@@ -1,0 +1,144 @@
+"""GPU parity of the fused decoder projection (``pg_decoder_gemv``) against
+a float32 PyTorch reference of the same op, and of the fused decoder step
+against the torch-op decoder step.
+
+Tolerances: the kernel accumulates in float32 in a different order than the
+reference and rounds once to FP16, so outputs agree to one FP16 rounding
+(rtol 2^-10) plus float32 accumulation noise; RMSNorm inputs may differ by
+one FP16 ulp where rsqrt rounds differently (rtol 2^-9), and a SwiGLU output
+compounds the roundings of gate and up (rtol 2^-8)."""
+
+from __future__ import annotations
+
+import pytest
+import torch
+import torch.nn.functional as F
+
+pytestmark = pytest.mark.gpu
+
+
+def _rand(gen, *shape, scale=1.0):
+    return (torch.randn(*shape, generator=gen) * scale).to(torch.float16)
+
+
+def _check(got, want32, rtol):
+    diff = (got.float() - want32).abs()
+    bound = want32.abs() * rtol + 2e-3
+    assert bool((diff <= bound).all()), f"max diff {float(diff.max()):.4g}"
+
+
+@pytest.mark.parametrize("n,k,batch", [(6144, 4096, 1), (4096, 4096, 2), (1001, 512, 1),
+                                       (3, 1024, 4), (32768, 4096, 1)])
+def test_projection_plain_and_residual(cuda, n, k, batch):
+    from pagegauge_amd.decoder import projection
+
+    print(f"projection n={n} k={k} batch={batch}", flush=True)
+    gen = torch.Generator().manual_seed(n + k + batch)
+    w = _rand(gen, n, k, scale=0.02).to(cuda)
+    x = _rand(gen, batch, k).to(cuda)
+    out = torch.empty(batch, n, device=cuda, dtype=torch.float16)
+    projection(w, x, out)
+    ref = x.float() @ w.float().t()
+    _check(out, ref, 2 ** -10)
+    res = _rand(gen, batch, n).to(cuda)
+    hidden = res.clone()
+    projection(w, x, hidden, residual=hidden)              # in place, as the decoder uses it
+    want = (res.float() + (x.float() @ w.float().t()).half().float()).half().float()
+    _check(hidden, want, 2 ** -9)
+    out32 = torch.empty(batch, n, device=cuda, dtype=torch.float32)
+    projection(w, x, out32)
+    assert torch.equal(out32, out.float())                # FP16 result widened
+
+
+@pytest.mark.parametrize("k,batch", [(4096, 1), (4096, 2), (512, 3)])
+def test_projection_rmsnorm_prologue(cuda, k, batch):
+    from pagegauge_amd.decoder import projection, rms_norm
+
+    gen = torch.Generator().manual_seed(k * batch)
+    n = 2048
+    w = _rand(gen, n, k, scale=0.02).to(cuda)
+    x = _rand(gen, batch, k, scale=3.0).to(cuda)
+    g = (1.0 + 0.25 * torch.randn(k, generator=gen)).to(torch.float16).to(cuda)
+    out = torch.empty(batch, n, device=cuda, dtype=torch.float16)
+    projection(w, x, out, norm_weight=g, eps=1e-5)
+    ref = rms_norm(x, g, 1e-5).float() @ w.float().t()
+    _check(out, ref, 2 ** -9)
+
+
+@pytest.mark.parametrize("n,k,batch,norm", [(28672, 4096, 1, True), (28672, 4096, 2, True),
+                                            (2048, 4096, 1, False), (1024, 512, 4, True)])
+def test_projection_swiglu_epilogue(cuda, n, k, batch, norm):
+    from pagegauge_amd.decoder import projection, rms_norm
+
+    gen = torch.Generator().manual_seed(n + k + batch)
+    w = _rand(gen, n, k, scale=0.02).to(cuda)
+    x = _rand(gen, batch, k, scale=2.0).to(cuda)
+    g = (1.0 + 0.25 * torch.randn(k, generator=gen)).to(torch.float16).to(cuda)
+    out = torch.empty(batch, n // 2, device=cuda, dtype=torch.float16)
+    projection(w, x, out, norm_weight=g if norm else None, swiglu=True)
+    xin = rms_norm(x, g, 1e-5) if norm else x
+    gate, up = (xin.float() @ w.float().t()).half().split(n // 2, dim=-1)
+    want = (F.silu(gate) * up).float()                    # FP16 ops as the decoder layer
+    _check(out, want, 2 ** -8)
+
+
+@pytest.mark.parametrize("k,batch", [(14336, 1), (14336, 4), (1024, 2)])
+def test_projection_down_with_residual(cuda, k, batch):
+    from pagegauge_amd.decoder import projection
+
+    gen = torch.Generator().manual_seed(k + batch)
+    n = 4096
+    w = _rand(gen, n, k, scale=0.02).to(cuda)
+    x = _rand(gen, batch, k).to(cuda)
+    res = _rand(gen, batch, n).to(cuda)
+    hidden = res.clone()
+    projection(w, x, hidden, residual=hidden)
+    want = (res.float() + (x.float() @ w.float().t()).half().float()).half().float()
+    _check(hidden, want, 2 ** -9)
+
+
+def test_projection_errors(cuda):
+    from pagegauge_amd.decoder import projection
+
+    w = torch.zeros(64, 4096, device=cuda, dtype=torch.float16)
+    x = torch.zeros(1, 4096, device=cuda, dtype=torch.float16)
+    out = torch.empty(1, 64, device=cuda, dtype=torch.float16)
+    with pytest.raises(RuntimeError, match="multiple of 512"):
+        projection(torch.zeros(64, 100, device=cuda, dtype=torch.float16),
+                   torch.zeros(1, 100, device=cuda, dtype=torch.float16), out)
+    with pytest.raises(RuntimeError, match="batch of 1 to 4"):
+        projection(w, torch.zeros(5, 4096, device=cuda, dtype=torch.float16),
+                   torch.empty(5, 64, device=cuda, dtype=torch.float16))
+    with pytest.raises(RuntimeError, match="LDS staging"):
+        big = torch.zeros(64, 10240, device=cuda, dtype=torch.float16)
+        projection(big, torch.zeros(4, 10240, device=cuda, dtype=torch.float16),
+                   torch.empty(4, 64, device=cuda, dtype=torch.float16))
+    with pytest.raises(RuntimeError, match="even n"):
+        projection(torch.zeros(63, 4096, device=cuda, dtype=torch.float16), x,
+                   torch.empty(1, 31, device=cuda, dtype=torch.float16), swiglu=True)
+    with pytest.raises(ValueError, match=r"\[B, N\]"):
+        projection(w, x, torch.empty(1, 65, device=cuda, dtype=torch.float16))
+
+
+def test_fused_decoder_step_matches_torch_op_step(cuda):
+    """Same weights and cache: fused projections vs torch ops, logits within
+    a few FP16 ulps (different accumulation orders only)."""
+    from pagegauge_amd import decoder as dec
+
+    cfg = dec.DecoderConfig(layers=2, intermediate=1024, vocab=512)
+    weights = dec.DecoderWeights(cfg, seed=3, device=cuda)
+    prompt = torch.randint(0, cfg.vocab, (512,), generator=torch.Generator().manual_seed(4))
+    first, _, decoders = dec.build_decoders(weights, prompt, 4, backends=("page_gauge",))
+    base = decoders["page_gauge"]
+    fused = dec.PageGaugeDecoder(weights, base.cache.clone(), "page_gauge", base.max_pages * 16,
+                                 base.rope_cos, base.rope_sin, fused=True)
+    plain = dec.PageGaugeDecoder(weights, base.cache.clone(), "page_gauge", base.max_pages * 16,
+                                 base.rope_cos, base.rope_sin, fused=False)
+    token = first
+    for i in range(3):
+        a = fused.step(token, 512 + i).clone()
+        b = plain.step(token, 512 + i)
+        scale = float(b.abs().max())
+        assert float((a - b).abs().max()) <= 0.02 * max(1.0, scale), i
+        assert float(F.cosine_similarity(a, b, dim=-1).min()) > 0.9999
+        token = b.argmax(-1)

@@ -589,3 +589,64 @@ def test_pins_catch_planted_mistakes():
     permuted = np.concatenate([query[h::8] for h in range(8)])       # heads regrouped
     wrong_gqa = oracle.attention_state(permuted, keys, vals, 0.088)[0]
     assert np.abs(right - wrong_gqa).max() > 1e-3
+
+
+# ---------------------------------------------------------------------------
+# heterogeneous one-table decode (a unified page table, INT8 then FP16)
+# ---------------------------------------------------------------------------
+
+# (old_tokens, total_tokens, ring_pages): the reference's nine CASES,
+# diagnostics/benchmark_heterogeneous_fa2_correctness.py:63-73
+HETERO_CASES = [(256, 256, 1), (0, 1, 2), (0, 15, 2), (0, 16, 2), (16, 17, 4), (16, 31, 4),
+                (16, 32, 4), (144, 176, 4), (144, 191, 4)]
+
+
+@pytest.mark.parametrize("old_tokens,total_tokens,ring_pages", HETERO_CASES)
+def test_heterogeneous_oracle_is_dense_softmax_over_logical_sequence(old_tokens, total_tokens,
+                                                                     ring_pages):
+    rng = np.random.default_rng(old_tokens * 1000 + total_tokens)
+    batch, hkv = 2, 2
+    total_pages = -(-total_tokens // 16)
+    old_pages = old_tokens // 16
+    k_codes = rng.integers(-127, 128, (batch * max(old_pages, 1), 16, hkv, 128)).astype(np.int8)
+    v_codes = rng.integers(-127, 128, k_codes.shape).astype(np.int8)
+    k_scale = (rng.random((k_codes.shape[0], hkv)) * 0.01 + 0.001).astype(np.float16)
+    v_scale = (rng.random((k_codes.shape[0], hkv)) * 0.01 + 0.001).astype(np.float16)
+    exact_k = np.full((batch * ring_pages, 16, hkv, 128), np.nan, np.float16)
+    exact_v = np.full_like(exact_k, np.nan)
+    query = (rng.standard_normal((batch, 4 * hkv, 128)) * 0.35).astype(np.float16)
+    center = (rng.standard_normal((batch, hkv, 128)) * 0.025).astype(np.float16)
+    indices, logical_k, logical_v = [], [], []
+    for r in range(batch):
+        ks, vs = [], []
+        for page in range(total_pages):
+            if page < old_pages:
+                pid = r * max(old_pages, 1) + page
+                indices.append(pid)
+                ks.append(k_codes[pid].astype(np.float64) * k_scale[pid].astype(np.float64)[None, :, None])
+                vs.append(v_codes[pid].astype(np.float64) * v_scale[pid].astype(np.float64)[None, :, None])
+            else:
+                pid = r * ring_pages + page % ring_pages
+                exact_k[pid] = rng.standard_normal((16, hkv, 128)) * 0.08
+                exact_v[pid] = rng.standard_normal((16, hkv, 128)) * 0.08
+                indices.append(pid)
+                ks.append(exact_k[pid].astype(np.float64))
+                vs.append(exact_v[pid].astype(np.float64))
+        logical_k.append(np.concatenate(ks)[:total_tokens])
+        logical_v.append(np.concatenate(vs)[:total_tokens])
+    last = (total_tokens - 1) % 16 + 1
+    indptr = np.arange(batch + 1) * total_pages
+    old_len = np.full(batch, old_tokens)
+    got16, lse, got = oracle.decode_heterogeneous(query, k_codes, v_codes, k_scale, v_scale,
+                                                  exact_k, exact_v, indptr, np.array(indices),
+                                                  np.full(batch, last), old_len, 128 ** -0.5,
+                                                  value_center=center)
+    for r in range(batch):
+        for h in range(4 * hkv):
+            g = h // 4
+            s = logical_k[r][:, g] @ query[r, h].astype(np.float64) / np.sqrt(128)
+            p = np.exp(s - s.max())
+            p /= p.sum()
+            want = p @ logical_v[r][:, g] + center[r, g].astype(np.float64)
+            assert np.abs(got[r, h] - want).max() < 1e-9
+    assert np.isfinite(got).all() and np.isfinite(lse).all()
