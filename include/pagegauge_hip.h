@@ -190,6 +190,8 @@ typedef struct pg_decode_plan {
   int32_t num_items;      /* work items (one workgroup each) */
   int32_t num_items_primary;
   int32_t max_items_per_request;
+  int32_t waves_per_block; /* KV heads (one wave each) per workgroup of the partial kernel */
+  int32_t reserved;
   int64_t items_offset;   /* byte offsets inside the workspace */
   int64_t item_ptr_offset;
   int64_t partial_offset;

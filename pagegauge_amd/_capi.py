@@ -12,7 +12,7 @@ import threading
 from pathlib import Path
 
 LIBRARY_PATH = Path(__file__).resolve().parent / "lib" / "libpagegauge_hip.so"
-ABI_VERSION = 1
+ABI_VERSION = 2
 
 PG_OK = 0
 PG_KV_INT8 = 0
@@ -41,6 +41,8 @@ class DecodePlan(ctypes.Structure):
         ("num_items", _i32),
         ("num_items_primary", _i32),
         ("max_items_per_request", _i32),
+        ("waves_per_block", _i32),
+        ("reserved", _i32),
         ("items_offset", _i64),
         ("item_ptr_offset", _i64),
         ("partial_offset", _i64),
