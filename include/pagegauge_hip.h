@@ -106,6 +106,27 @@ int32_t pg_rope_append_page_gauge_positions(
     int32_t code_pages_per_request, int64_t rope_row_stride, int32_t rope_rows,
     void* stream);
 
+/* Serving-table variant of pg_rope_append_page_gauge_positions (no kernel
+ * of the reference: its serving prototype leaves the device scatter open,
+ * experiments/mlsys2027/serving_v1/pagegauge_vllm/decode_metadata.py:1-5).
+ * Row r appends the token at positions[r] into row positions[r] % 16 of
+ * exact page exact_page_ids[r] (FP16 centered) and, on the page's 16th
+ * token, quantises that exact page into code page code_page_ids[r]; both ids
+ * come from the caller's block tables (any physical page, any exact slot).
+ * Rows with a negative id or one outside [0, num_exact_pages) /
+ * [0, num_code_pages) are skipped.  RoPE rows come from the [rope_rows, 128]
+ * tables at positions[r]. */
+int32_t pg_rope_append_page_gauge_slots(
+    const void* query, const void* key, const void* value, const void* cosine,
+    const void* sine, const int32_t* positions, const int32_t* exact_page_ids,
+    const int32_t* code_page_ids, const void* key_center, const void* value_center,
+    int64_t center_batch_stride, void* rotated_query, void* exact_key_pages,
+    void* exact_value_pages, int8_t* key_codes, int8_t* value_codes, void* key_scales,
+    void* value_scales, int64_t query_batch_stride, int64_t key_batch_stride,
+    int64_t value_batch_stride, int32_t batch_size, int32_t query_heads, int32_t kv_heads,
+    int64_t num_exact_pages, int64_t num_code_pages, int64_t rope_row_stride,
+    int32_t rope_rows, void* stream);
+
 /* Per-request FP16 append at (page_ids[r], page_offsets[r]).  Replaces the
  * Triton append_kv (scripts/benchmark_page_gauge_overheads.py:86-109,
  * :242-269).  key/value contiguous [B, H, 128]. */

@@ -47,6 +47,8 @@ PINNED = {
     "quantize_page_gauge": "torch transcription of scripts/benchmark_flashinfer_page_affine_int8.py:256-278",
     "quantize_completed_kv_pages": "torch transcription of scripts/benchmark_page_gauge_overheads.py:23-83",
     "append_finalize_page_gauge": "equivalence with rope_append_page_gauge at identity RoPE",
+    "rope_append_page_gauge_slots": "equivalence with rope_append_page_gauge_positions when the "
+    "ids are the request-major slots",
     "decode": "torch float64 softmax attention; logsumexp identity; merge associativity",
     "merge_state": "decode(A u B) == merge(decode(A), decode(B))",
     "exact_tail_merge_center": "torch oracle of tests/test_page_gauge_append_extension.py:628-657",
@@ -262,6 +264,33 @@ def rope_append_page_gauge_positions(query, key, value, cosine_table, sine_table
             key_scales, value_scales,
             request * exact_pages_per_request + local,
             request * code_pages_per_request + page, token)
+
+
+def rope_append_page_gauge_slots(query, key, value, cosine_table, sine_table, positions,
+                                 exact_page_ids, code_page_ids, key_center, value_center,
+                                 rotated_query, exact_key_pages, exact_value_pages, key_codes,
+                                 value_codes, key_scales, value_scales) -> None:
+    """Serving-table variant: row ``r`` appends at ``positions[r]`` into exact
+    page ``exact_page_ids[r]`` and finalizes into code page ``code_page_ids[r]``
+    (the ids of the serving block tables,
+    experiments/mlsys2027/serving_v1/pagegauge_vllm/decode_metadata.py:50-60);
+    the arithmetic is ``rope_append_page_gauge``'s.  Negative or out-of-pool
+    ids skip the row."""
+    rope_rows = cosine_table.shape[0]
+    for request in range(query.shape[0]):
+        position = int(positions[request])
+        exact_page, code_page = int(exact_page_ids[request]), int(code_page_ids[request])
+        if not (0 <= position < rope_rows and 0 <= exact_page < exact_key_pages.shape[0]
+                and 0 <= code_page < key_codes.shape[0]):
+            continue
+        cosine, sine = cosine_table[position], sine_table[position]
+        rotated_query[request] = rope_rotate(query[request], cosine, sine)
+        rotated_key = rope_rotate(key[request], cosine, sine)
+        _append_centered_and_finalize(
+            rotated_key, value[request],
+            _center_for(key_center, request), _center_for(value_center, request),
+            exact_key_pages, exact_value_pages, key_codes, value_codes,
+            key_scales, value_scales, exact_page, code_page, position % PAGE)
 
 
 def append_kv(key, value, key_pages, value_pages, page_ids, page_offsets) -> None:

@@ -62,6 +62,9 @@ PROTOTYPES = {
     "pg_rope_append_page_gauge_positions": (_i32, [_p, _p, _p, _p, _p, _p, _p, _p, _i64, _p, _p,
                                                    _p, _p, _p, _p, _p, _i64, _i64, _i64, _i32,
                                                    _i32, _i32, _i32, _i32, _i32, _i64, _i32, _p]),
+    "pg_rope_append_page_gauge_slots": (_i32, [_p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _i64, _p, _p,
+                                               _p, _p, _p, _p, _p, _i64, _i64, _i64, _i32, _i32,
+                                               _i32, _i64, _i64, _i64, _i32, _p]),
     "pg_append_kv": (_i32, [_p, _p, _p, _p, _p, _p, _i32, _i32, _i32, _p]),
     "pg_append_finalize_page_gauge": (_i32, [_p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _i32,
                                              _i32, _i32, _p]),

@@ -51,6 +51,10 @@ struct UpdateParams {
   int host_position;
   const int32_t* device_position;  // scalar position (graph replay)
   const int32_t* positions;        // per-request positions
+  const int32_t* exact_page_ids;   // per-request exact page of the position (serving tables)
+  const int32_t* code_page_ids;    // per-request code page of the position
+  int64_t num_exact_pages;         // pool sizes for the explicit ids (out of range: no-op)
+  int64_t num_code_pages;
   int64_t rope_row_stride;
   int rope_rows;
   int row_blocks;                  // blocks per request
@@ -168,7 +172,10 @@ __global__ __launch_bounds__(kWave * kWavesPerBlock) void rope_append_kernel(Upd
     position = p.host_position;
     dynamic = false;
   }
-  const int capacity = (kPageGauge ? p.code_pages_per_request : p.pages_per_request) * kPageSize;
+  const bool explicit_pages = p.exact_page_ids != nullptr;
+  const int capacity = explicit_pages ? INT32_MAX
+                                      : (kPageGauge ? p.code_pages_per_request : p.pages_per_request) *
+                                            kPageSize;
   if (position < 0 || position >= capacity || (dynamic && position >= p.rope_rows)) return;
   const uint16_t* cosine = p.cosine;
   const uint16_t* sine = p.sine;
@@ -200,10 +207,19 @@ __global__ __launch_bounds__(kWave * kWavesPerBlock) void rope_append_kernel(Upd
     store_pair(p.key_pages + dst, rk.lo, rk.hi);
     store_pair(p.value_pages + dst, rv.lo, rv.hi);
   } else {
-    const int tail_pages = p.pages_per_request - p.exact_sink_pages;
-    const int local = page < p.exact_sink_pages ? page : p.exact_sink_pages + page % tail_pages;
-    const int64_t exact_page = static_cast<int64_t>(request) * p.pages_per_request + local;
-    const int64_t code_page = static_cast<int64_t>(request) * p.code_pages_per_request + page;
+    int64_t exact_page, code_page;
+    if (explicit_pages) {
+      exact_page = p.exact_page_ids[request];
+      code_page = p.code_page_ids[request];
+      if (exact_page < 0 || code_page < 0 || exact_page >= p.num_exact_pages ||
+          code_page >= p.num_code_pages)
+        return;                                          // row not scheduled / out of the pools
+    } else {
+      const int tail_pages = p.pages_per_request - p.exact_sink_pages;
+      const int local = page < p.exact_sink_pages ? page : p.exact_sink_pages + page % tail_pages;
+      exact_page = static_cast<int64_t>(request) * p.pages_per_request + local;
+      code_page = static_cast<int64_t>(request) * p.code_pages_per_request + page;
+    }
     const uint16_t* kc = p.key_center + request * p.center_batch_stride + head * kHeadDim + 2 * lane;
     const uint16_t* vc = p.value_center + request * p.center_batch_stride + head * kHeadDim + 2 * lane;
     const Half2Bits ckc = load_pair(kc);
@@ -618,6 +634,41 @@ extern "C" int32_t pg_rope_append_page_gauge_positions(
       value_scales, query_batch_stride, key_batch_stride, value_batch_stride, batch_size,
       query_heads, kv_heads, exact_pages_per_request, exact_sink_pages, code_pages_per_request);
   p.positions = positions;
+  p.rope_row_stride = rope_row_stride;
+  p.rope_rows = rope_rows;
+  return launch_rope_append(p, true, as_stream(stream));
+}
+
+extern "C" int32_t pg_rope_append_page_gauge_slots(
+    const void* query, const void* key, const void* value, const void* cosine, const void* sine,
+    const int32_t* positions, const int32_t* exact_page_ids, const int32_t* code_page_ids,
+    const void* key_center, const void* value_center, int64_t center_batch_stride,
+    void* rotated_query, void* exact_key_pages, void* exact_value_pages, int8_t* key_codes,
+    int8_t* value_codes, void* key_scales, void* value_scales, int64_t query_batch_stride,
+    int64_t key_batch_stride, int64_t value_batch_stride, int32_t batch_size,
+    int32_t query_heads, int32_t kv_heads, int64_t num_exact_pages, int64_t num_code_pages,
+    int64_t rope_row_stride, int32_t rope_rows, void* stream) {
+  clear_error();
+  if (int32_t rc = check_common(batch_size, query_heads, kv_heads)) return rc;
+  if (num_exact_pages <= 0 || num_code_pages <= 0)
+    return fail(PG_ERROR_INVALID_ARGUMENT, "exact and code page pools must be non-empty");
+  if (any_null({query, key, value, cosine, sine, positions, exact_page_ids, code_page_ids,
+                key_center, value_center, rotated_query, exact_key_pages, exact_value_pages,
+                key_codes, value_codes, key_scales, value_scales}))
+    return fail(PG_ERROR_INVALID_ARGUMENT, "null tensor pointer");
+  if (rope_rows <= 0)
+    return fail(PG_ERROR_INVALID_ARGUMENT,
+                "dynamic RoPE tables must be matching [positions,128] tensors");
+  UpdateParams p = page_gauge_params(
+      query, key, value, cosine, sine, key_center, value_center, center_batch_stride,
+      rotated_query, exact_key_pages, exact_value_pages, key_codes, value_codes, key_scales,
+      value_scales, query_batch_stride, key_batch_stride, value_batch_stride, batch_size,
+      query_heads, kv_heads, 1, 0, 1);
+  p.positions = positions;
+  p.exact_page_ids = exact_page_ids;
+  p.code_page_ids = code_page_ids;
+  p.num_exact_pages = num_exact_pages;
+  p.num_code_pages = num_code_pages;
   p.rope_row_stride = rope_row_stride;
   p.rope_rows = rope_rows;
   return launch_rope_append(p, true, as_stream(stream));

@@ -280,6 +280,40 @@ class PageGaugeAppendExtension:
                                 value_codes, key_scales, value_scales, exact_sink_pages, 0,
                                 None, positions, "rope_append_page_gauge_positions")
 
+    def rope_append_page_gauge_slots(self, query, key, value, cosine, sine, positions,
+                                     exact_page_ids, code_page_ids, key_center, value_center,
+                                     rotated_query, exact_key_pages, exact_value_pages,
+                                     key_codes, value_codes, key_scales, value_scales) -> None:
+        """Per-request positions with explicit exact and code page ids (device
+        int32 [B] each), as a serving block table gives them; centers are
+        per row ([B,Hkv,128], or [Hkv,128] for batch one)."""
+        self._dynamic_head_checks(query, key, value, rotated_query, exact_key_pages,
+                                  exact_value_pages)
+        _check_tensor(cosine, "cosine", torch.float16, 2)
+        _check_tensor(sine, "sine", torch.float16, 2)
+        _require(cosine.shape == sine.shape and cosine.size(0) > 0 and cosine.size(1) == HEAD_DIM,
+                 "dynamic RoPE tables must be matching [positions,128] tensors")
+        batch = query.size(0)
+        for tensor, name in ((positions, "positions"), (exact_page_ids, "exact_page_ids"),
+                             (code_page_ids, "code_page_ids")):
+            _check_tensor(tensor, name, torch.int32, 1)
+            _require(tensor.numel() == batch, f"{name} must contain one int32 per request")
+        kv_heads = key.size(1)
+        center_stride = _check_centers(key_center, value_center, batch, kv_heads)
+        _check_codes(key_codes, value_codes, key_scales, value_scales, kv_heads)
+        _require(key_scales.shape == value_scales.shape and key_scales.size(0) == key_codes.size(0)
+                 and key_scales.size(1) == kv_heads, "scales must be [pages,Hkv]")
+        _capi.check(self._lib.pg_rope_append_page_gauge_slots(
+            query.data_ptr(), key.data_ptr(), value.data_ptr(), cosine.data_ptr(),
+            sine.data_ptr(), positions.data_ptr(), exact_page_ids.data_ptr(),
+            code_page_ids.data_ptr(), key_center.data_ptr(), value_center.data_ptr(),
+            center_stride, rotated_query.data_ptr(), exact_key_pages.data_ptr(),
+            exact_value_pages.data_ptr(), key_codes.data_ptr(), value_codes.data_ptr(),
+            key_scales.data_ptr(), value_scales.data_ptr(), query.stride(0), key.stride(0),
+            value.stride(0), batch, query.size(1), kv_heads, exact_key_pages.size(0),
+            key_codes.size(0), cosine.stride(0), cosine.size(0), _stream()),
+            "rope_append_page_gauge_slots")
+
     # -- fused exact tail (tests/page_gauge_append_extension.cu:950-1028) ---
     def exact_tail_merge_center(self, query, exact_key_pages, exact_value_pages,
                                 exact_page_indices, exact_last_page_len, old_output, old_lse,
