@@ -16,10 +16,13 @@ overwriting ring slots", decode_metadata.py:1-5) is here:
   code page when its 16th token lands, so every page that later ages out of
   the tail ring already has codes), and the INT8-history and exact CSR tables
   for ``PageGaugeSegmentedDecode`` (K1);
-* ``dense_pool_views`` / ``allocate_sidecars`` give the pools and sidecars in
-  the layouts the kernels read.
+* ``dense_pool_views`` / ``from_engine_layer`` / ``zero_physical_pages`` /
+  ``allocate_sidecars`` give the pools and sidecars in the layouts the kernels
+  read (cache_views.py:1-62).
 
-CPU bookkeeping only; streams and events are the caller's.
+The request lifecycle and scheduler transactions built on ``RequestSlots``
+are in ``serving_bridge``.  CPU bookkeeping only; streams and events are the
+caller's.
 """
 
 from __future__ import annotations
@@ -122,6 +125,17 @@ class RequestSlots:
         self.generations = [0] * maximum_requests
         self.states: dict[str, State] = {}
         self.page_owner: dict[int, Lease] = {}
+
+    def clone(self) -> "RequestSlots":
+        """Independent copy of the bookkeeping (leases and states are immutable,
+        so the containers are all that is copied)."""
+        other = RequestSlots.__new__(RequestSlots)
+        other.policy = self.policy
+        other.free = list(self.free)
+        other.generations = list(self.generations)
+        other.states = dict(self.states)
+        other.page_owner = dict(self.page_owner)
+        return other
 
     def _pages(self, physical_pages, count: int) -> tuple:
         pages = tuple(physical_pages)
@@ -380,6 +394,37 @@ def dense_pool_views(raw, physical_pages: int, kv_heads: int, head_dim: int = 12
                                                                                  kv_heads),
         "value_scales": raw[2 * codes + scales:].view(torch.float16).view(physical_pages, kv_heads),
     }
+
+
+def from_engine_layer(layer, physical_pages: int, kv_heads: int) -> dict:
+    """The planes of a compact packed engine layer [pages, Hkv, 1, 2*16*128+4]
+    uint8, reinterpreted in place (cache_views.py:30-41)."""
+    import torch
+
+    expected = (physical_pages, kv_heads, 1, 2 * PAGE * 128 + 4)
+    if layer.dtype != torch.uint8 or tuple(layer.shape) != expected or not layer.is_contiguous():
+        raise ValueError("Compact packed engine layer required; copying is forbidden")
+    return dense_pool_views(layer.view(-1), physical_pages, kv_heads)
+
+
+def zero_physical_pages(views: dict, page_ids) -> None:
+    """Clear fresh pages in all four planes on the current stream (an index
+    fill kernel per plane) before they are used (cache_views.py:44-62)."""
+    import torch
+
+    planes = tuple(views[name] for name in ("key_codes", "value_codes", "key_scales",
+                                            "value_scales"))
+    first = planes[0]
+    pages = tuple(page_ids)
+    if (any(t.device != first.device or t.shape[0] != first.shape[0] for t in planes)
+            or any(type(p) is not int or not 0 <= p < first.shape[0] for p in pages)
+            or len(set(pages)) != len(pages)):
+        raise ValueError("Invalid physical pages or inconsistent pool views")
+    if not pages:
+        return
+    index = torch.tensor(pages, dtype=torch.int64, device=first.device)
+    for plane in planes:
+        plane.index_fill_(0, index, 0)
 
 
 def allocate_sidecars(layout: Layout, *, device, cache_budget_bytes: int) -> dict:
