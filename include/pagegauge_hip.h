@@ -212,6 +212,18 @@ typedef struct pg_decode_plan {
   int32_t num_items_primary;
   int32_t max_items_per_request;
   int32_t waves_per_block; /* KV heads (one wave each) per workgroup of the partial kernel */
+  /* closed_form = 1 (one request): work item i is derived from the block
+   * index instead of being loaded.  The FP16 tail segment's cf_tail_items
+   * items come first, then the primary segment's; segment s with n pages in
+   * c items gives item k the pages [begin + k*(n/c) + min(k, n%c), +
+   * n/c + (k < n%c)).  The planner sets it only when this reproduces every
+   * work item it wrote. */
+  int32_t closed_form;
+  int32_t cf_tail_items;
+  int32_t cf_tail_begin;
+  int32_t cf_tail_pages;
+  int32_t cf_primary_begin;
+  int32_t cf_primary_pages;
   int32_t reserved;
   int64_t items_offset;   /* byte offsets inside the workspace */
   int64_t item_ptr_offset;

@@ -12,7 +12,7 @@ import threading
 from pathlib import Path
 
 LIBRARY_PATH = Path(__file__).resolve().parent / "lib" / "libpagegauge_hip.so"
-ABI_VERSION = 2
+ABI_VERSION = 3
 
 PG_OK = 0
 PG_KV_INT8 = 0
@@ -42,6 +42,12 @@ class DecodePlan(ctypes.Structure):
         ("num_items_primary", _i32),
         ("max_items_per_request", _i32),
         ("waves_per_block", _i32),
+        ("closed_form", _i32),
+        ("cf_tail_items", _i32),
+        ("cf_tail_begin", _i32),
+        ("cf_tail_pages", _i32),
+        ("cf_primary_begin", _i32),
+        ("cf_primary_pages", _i32),
         ("reserved", _i32),
         ("items_offset", _i64),
         ("item_ptr_offset", _i64),

@@ -104,7 +104,44 @@ struct DecodeArgs {
   int waves_per_block;
   int max_items;      // partial rows per (request, head)
   float sm_scale_log2;
+  // one-request plans: work items from the block index (no item load)
+  int closed_form;
+  int cf_items;
+  int cf_tail_items;
+  int cf_tail_begin;
+  int cf_tail_pages;
+  int cf_primary_begin;
+  int cf_primary_pages;
+  int cf_primary_kind;
 };
+
+// Work item ``i`` of a one-request plan: the FP16 tail segment's items
+// first, then the primary segment's; segment pages [base, base + n) in c
+// nearly equal chunks (the first n % c one page longer), as the planner
+// cuts them.
+__host__ __device__ __forceinline__ WorkItem closed_form_item(int i, int items, int tail_items,
+                                                              int tail_begin, int tail_pages,
+                                                              int primary_begin, int primary_pages,
+                                                              int primary_kind) {
+  const bool tail = i < tail_items;
+  const int n = tail ? tail_pages : primary_pages;
+  const int c = tail ? tail_items : items - tail_items;
+  const int k = tail ? i : i - tail_items;
+  const int base = tail ? tail_begin : primary_begin;
+  const int q = n / c;
+  const int r = n % c;
+  WorkItem it{};
+  it.request = 0;
+  it.kind = tail ? PG_KV_FP16 : primary_kind;
+  it.segment = tail ? 1 : 0;
+  it.page_begin = base + k * q + (k < r ? k : r);
+  it.page_end = it.page_begin + q + (k < r ? 1 : 0);
+  it.last_page = base + n - 1;
+  it.item_in_request = i;
+  it.items_in_request = items;
+  it.request_page_begin = base;
+  return it;
+}
 
 // Per-lane softmax/output state of one KV head (4 query heads).
 // Lane l owns head h = l/16; o[nb] is output dim 8*(l%16) + nb.
@@ -748,7 +785,11 @@ __global__ __launch_bounds__(kWave * kMaxWavesPerBlock) void decode_partial_kern
   const int wave = threadIdx.x / kWave;
   const int lane = threadIdx.x % kWave;
   const int kv = blockIdx.y * a.waves_per_block + wave;
-  const WorkItem it = a.items[blockIdx.x];
+  const WorkItem it = a.closed_form
+                          ? closed_form_item(blockIdx.x, a.cf_items, a.cf_tail_items, a.cf_tail_begin,
+                                             a.cf_tail_pages, a.cf_primary_begin, a.cf_primary_pages,
+                                             a.cf_primary_kind)
+                          : a.items[blockIdx.x];
   uint8_t* lds = lds_all + wave * kLdsPerWave;
   HeadState st;
   init_state(st);
@@ -1072,6 +1113,29 @@ int32_t build_plan(const int32_t* host_indptr, const int32_t* host_last_page_len
   p.max_items_per_request = max_per_request;
   p.waves_per_block = waves_per_block_for(num_kv_heads, static_cast<int64_t>(items.size()),
                                           num_cus > 0 ? num_cus : 256);
+  // One request: describe the items in closed form when the formula gives
+  // exactly the table (the kernel then skips the work-item load).
+  if (batch_size == 1 && !items.empty()) {
+    p.cf_tail_items = static_cast<int32_t>(items.size()) - p.num_items_primary;
+    if (host_tail_indptr) {
+      p.cf_tail_begin = host_tail_indptr[0];
+      p.cf_tail_pages = host_tail_indptr[1] - host_tail_indptr[0];
+    }
+    p.cf_primary_begin = host_indptr[0];
+    p.cf_primary_pages = host_indptr[1] - host_indptr[0];
+    bool same = p.num_items_primary > 0 || p.cf_tail_items > 0;
+    for (size_t i = 0; same && i < items.size(); ++i) {
+      const WorkItem cf = closed_form_item(static_cast<int>(i), p.num_items, p.cf_tail_items,
+                                           p.cf_tail_begin, p.cf_tail_pages, p.cf_primary_begin,
+                                           p.cf_primary_pages, primary_kind);
+      same = std::memcmp(&cf, &items[i], sizeof(WorkItem)) == 0;
+    }
+    p.closed_form = same ? 1 : 0;
+    if (!same) {
+      p.cf_tail_items = p.cf_tail_begin = p.cf_tail_pages = 0;
+      p.cf_primary_begin = p.cf_primary_pages = 0;
+    }
+  }
   p.items_offset = 0;
   p.item_ptr_offset = align_up(n_items * static_cast<int64_t>(sizeof(WorkItem)), 256);
   p.partial_offset = p.item_ptr_offset + align_up((batch_size + 1) * 4, 256);
@@ -1226,6 +1290,22 @@ int32_t launch_partial(const pg_decode_plan_t* plan, const void* query,
     return fail(PG_ERROR_INVALID_ARGUMENT, "plan has an invalid waves_per_block");
   a.max_items = std::max(1, plan->max_items_per_request);
   a.sm_scale_log2 = sm_scale * 1.4426950408889634f;
+  if (plan->closed_form) {
+    if (plan->batch_size != 1 || plan->cf_tail_items < 0 || plan->cf_tail_items > plan->num_items ||
+        plan->cf_tail_pages < plan->cf_tail_items || plan->cf_tail_pages < 0 ||
+        plan->cf_primary_pages < plan->num_items - plan->cf_tail_items ||
+        (plan->cf_tail_items == 0) != (plan->cf_tail_pages == 0) ||
+        (plan->num_items - plan->cf_tail_items == 0) != (plan->cf_primary_pages == 0))
+      return fail(PG_ERROR_INVALID_ARGUMENT, "plan has an inconsistent closed-form description");
+    a.closed_form = 1;
+    a.cf_items = plan->num_items;
+    a.cf_tail_items = plan->cf_tail_items;
+    a.cf_tail_begin = plan->cf_tail_begin;
+    a.cf_tail_pages = plan->cf_tail_pages;
+    a.cf_primary_begin = plan->cf_primary_begin;
+    a.cf_primary_pages = plan->cf_primary_pages;
+    a.cf_primary_kind = plan->primary_kind;
+  }
   const dim3 grid(plan->num_items, plan->num_kv_heads / a.waves_per_block);
   if (start_event || stop_event) {
     // The events take the dispatch's own begin/end timestamps.

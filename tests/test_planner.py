@@ -98,3 +98,44 @@ def test_plan_rejects_too_many_items_per_request():
     with pytest.raises(RuntimeError, match="too many splits"):
         plan_work_items([0, 5000], [16], split_pages=1)
 
+
+
+def _closed_form_items(plan, kind):
+    """Work items from a plan's closed-form description (the kernel's rule)."""
+    rows = []
+    for i in range(plan.num_items):
+        tail = i < plan.cf_tail_items
+        n = plan.cf_tail_pages if tail else plan.cf_primary_pages
+        c = plan.cf_tail_items if tail else plan.num_items - plan.cf_tail_items
+        k = i if tail else i - plan.cf_tail_items
+        base = plan.cf_tail_begin if tail else plan.cf_primary_begin
+        q, r = divmod(n, c)
+        begin = base + k * q + min(k, r)
+        rows.append([0, 1 if tail else kind, int(tail), begin, begin + q + (k < r), base + n - 1,
+                     i, plan.num_items, base, 0, 0, 0])
+    return rows
+
+
+@pytest.mark.parametrize("old,tail,split,tail_split,dtype", [
+    ([0, 3056], [0, 16], 0, 0, torch.int8),          # B1/49K balanced
+    ([5, 1014], [3, 19], 0, 0, torch.int8),          # offsets into shared tables
+    ([0, 3056], [0, 16], 11, 3, torch.int8),         # fixed splits with remainders
+    ([0, 7], [0, 16], 0, 0, torch.int8),
+    ([0, 1009], None, 0, 0, torch.float16),          # FP16 pages, no tail
+    ([2, 900], None, 5, 0, "heterogeneous"),
+    ([0, 0], [0, 16], 0, 0, torch.int8),             # tail only
+])
+def test_one_request_plans_are_closed_form(old, tail, split, tail_split, dtype):
+    plan, items, _ = plan_work_items(old, [16], tail, None if tail is None else [16],
+                                     kv_data_type=dtype, split_pages=split,
+                                     tail_split_pages=tail_split)
+    kind = {torch.int8: 0, torch.float16: 1, "heterogeneous": 2}[dtype]
+    assert plan.closed_form == 1
+    assert plan.cf_tail_items == plan.num_items - plan.num_items_primary
+    assert _closed_form_items(plan, kind) == items.tolist()
+
+
+def test_batches_keep_the_item_table():
+    plan, _, _ = plan_work_items([0, 100, 240], [16, 16], [0, 16, 32], [16, 16])
+    assert plan.closed_form == 0
+    assert (plan.cf_tail_items, plan.cf_primary_pages) == (0, 0)
