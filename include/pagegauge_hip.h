@@ -328,6 +328,37 @@ int32_t pg_decode_run_heterogeneous(const pg_decode_plan_t* plan, const void* qu
                                     int64_t center_batch_stride, void* out, float* lse,
                                     float sm_scale, void* workspace, void* stream);
 
+/* pg_decode_run / pg_decode_run_heterogeneous plus the completed-page
+ * finalize of the decode step's cache update.  No reference counterpart as
+ * one call: the finalize of rope_append_page_gauge(_dynamic)
+ * (tests/page_gauge_append_extension.cu:327-382), moved into the FP16 pass
+ * over the exact pages for callers whose cache update ran without it
+ * (pg_decoder_qkv_rope_append).  When the token at positions[r *
+ * position_stride] completed its page (position % 16 == 15, and that page is
+ * the last page of r's FP16 segment), the wave that attends to the page
+ * writes its INT8 codes and scales into code page r * code_pages_per_request
+ * + position / 16 of k_cache/v_cache and k_scale/v_scale: the same codes and
+ * scales as that finalize.  Attention outputs are those of the run without
+ * it. */
+int32_t pg_decode_run_finalize(const pg_decode_plan_t* plan, const void* query,
+                               int64_t query_batch_stride, const void* k_cache,
+                               const void* v_cache, const void* k_scale, const void* v_scale,
+                               const int32_t* indices, const int32_t* last_page_len,
+                               const void* tail_k, const void* tail_v,
+                               const int32_t* tail_indices, const int32_t* tail_last_len,
+                               const void* value_center, int64_t center_batch_stride, void* out,
+                               float* lse, float sm_scale, void* workspace,
+                               const int32_t* positions, int32_t position_stride,
+                               int32_t code_pages_per_request, void* stream);
+int32_t pg_decode_run_heterogeneous_finalize(
+    const pg_decode_plan_t* plan, const void* query, int64_t query_batch_stride,
+    const void* k_codes, const void* v_codes, const void* k_scale, const void* v_scale,
+    const void* exact_k, const void* exact_v, const int32_t* indices,
+    const int32_t* last_page_len, const int32_t* old_kv_len, const void* value_center,
+    int64_t center_batch_stride, void* out, float* lse, float sm_scale, void* workspace,
+    const int32_t* positions, int32_t position_stride, int32_t code_pages_per_request,
+    void* stream);
+
 /* The two launches of pg_decode_run, for callers that schedule them
  * separately (e.g. to time the partial kernel, or to overlap the combine
  * with other work): pg_decode_run_partial writes one unnormalised partial
@@ -425,6 +456,34 @@ int32_t pg_decoder_gemv(const void* weight, int32_t n, int32_t k, const void* x,
                         int64_t x_stride, int32_t batch, const void* norm_weight, float eps,
                         int32_t swiglu, const void* residual, int64_t residual_stride, void* out,
                         int64_t out_stride, int32_t out_f32, void* stream);
+
+/* The QKV projection of a decode step fused with its cache update: the
+ * decoder layer's qkv F.linear (with the input RMSNorm, as pg_decoder_gemv)
+ * followed by rope_append_page_gauge_dynamic / rope_append_fp16_dynamic
+ * (tests/page_gauge_append_extension.cu:244-383, :686-948) without the page
+ * finalize, which pg_decode_run_finalize performs.  weight [(Hq + 2 Hkv)*128,
+ * 4096] (query rows, key rows, value rows); for batch row b at position p =
+ * positions[b * position_stride]:
+ *   rotated_query[b, h] = RoPE(q) with the cosine/sine rows p, each element
+ *     rn16(rn16(x*c) + rn16(partner*s)) from the fp16-rounded projection;
+ *   key_center != NULL (PageGauge): the rotated key and the value, centered
+ *     as fp16(f32(x) - f32(center)), go to token p % 16 of exact page
+ *     b * pages_per_request + (page < sink_pages ? page : sink_pages + page %
+ *     (pages_per_request - sink_pages)), page = p / 16;
+ *   key_center == NULL: rotated key and value go to token p % 16 of page
+ *     b * pages_per_request + p / 16 of key_pages/value_pages;
+ * a position outside [0, capacity_tokens) or the RoPE table writes nothing.
+ * Bit-identical to the projection followed by the cache-update launch. */
+int32_t pg_decoder_qkv_rope_append(const void* weight, int32_t k, const void* x,
+                                   int64_t x_stride, int32_t batch, const void* norm_weight,
+                                   float eps, int32_t query_heads, int32_t kv_heads,
+                                   const void* cosine, const void* sine, int64_t rope_row_stride,
+                                   int32_t rope_rows, const int32_t* positions,
+                                   int32_t position_stride, void* rotated_query, void* key_pages,
+                                   void* value_pages, const void* key_center,
+                                   const void* value_center, int64_t center_batch_stride,
+                                   int32_t pages_per_request, int32_t sink_pages,
+                                   int32_t capacity_tokens, void* stream);
 
 #ifdef __cplusplus
 }

@@ -95,9 +95,18 @@ PROTOTYPES = {
                                            _p, _p, _p, _p, _p, _p, _f32, _p, _p, _p, _p]),
     "pg_decode_run_heterogeneous": (_i32, [ctypes.POINTER(DecodePlan), _p, _i64, _p, _p, _p, _p,
                                            _p, _p, _p, _p, _p, _p, _i64, _p, _p, _f32, _p, _p]),
+    "pg_decode_run_finalize": (_i32, [ctypes.POINTER(DecodePlan), _p, _i64, _p, _p, _p, _p, _p,
+                                      _p, _p, _p, _p, _p, _p, _i64, _p, _p, _f32, _p, _p, _i32,
+                                      _i32, _p]),
+    "pg_decode_run_heterogeneous_finalize": (_i32, [ctypes.POINTER(DecodePlan), _p, _i64, _p, _p,
+                                                    _p, _p, _p, _p, _p, _p, _p, _p, _i64, _p, _p,
+                                                    _f32, _p, _p, _i32, _i32, _p]),
     "pg_decode_run_combine": (_i32, [ctypes.POINTER(DecodePlan), _p, _i64, _p, _p, _p, _p]),
     "pg_decoder_gemv": (_i32, [_p, _i32, _i32, _p, _i64, _i32, _p, _f32, _i32, _p, _i64, _p, _i64,
                                _i32, _p]),
+    "pg_decoder_qkv_rope_append": (_i32, [_p, _i32, _p, _i64, _i32, _p, _f32, _i32, _i32, _p, _p,
+                                          _i64, _i32, _p, _i32, _p, _p, _p, _p, _p, _i64, _i32,
+                                          _i32, _i32, _p]),
     "pg_merge_state_in_place": (_i32, [_p, _p, _p, _p, _p, _i32, _i32, _i32, _p]),
     "pg_exact_tail_merge_center": (_i32, [_p, _p, _p, _p, _p, _p, _p, _p, _i64, _i32, _i32, _i32,
                                           _i32, _f32, _p]),

@@ -113,6 +113,15 @@ struct DecodeArgs {
   int cf_primary_begin;
   int cf_primary_pages;
   int cf_primary_kind;
+  // decode-step finalize: the FP16 tail pass quantises the page that the
+  // token at finalize_positions[request * finalize_position_stride] completed
+  const int32_t* finalize_positions;
+  int finalize_position_stride;
+  int code_pages_per_request;
+  int8_t* finalize_k_codes;
+  int8_t* finalize_v_codes;
+  uint16_t* finalize_k_scale;
+  uint16_t* finalize_v_scale;
 };
 
 // Work item ``i`` of a one-request plan: the FP16 tail segment's items
@@ -482,6 +491,72 @@ __device__ __forceinline__ void int8_chunk(const DecodeArgs& a, const WorkItem& 
 // ---------------------------------------------------------------------------
 __device__ __forceinline__ uint32_t word_of(v4u v, int i) { return v[i]; }
 
+// Sign-symmetric rounding of x / scale to [-127, 127] and the stored page
+// scale fp16(max(|x|max / 127, 2^-20)): the cache update's finalize
+// (tests/page_gauge_append_extension.cu:327-382).
+__device__ __forceinline__ uint32_t symmetric_code_byte(float quotient) {
+  int code = quotient >= 0.0f ? static_cast<int>(floorf(quotient + 0.5f))
+                              : -static_cast<int>(floorf(-quotient + 0.5f));
+  code = max(-127, min(127, code));
+  return static_cast<uint32_t>(static_cast<uint8_t>(static_cast<int8_t>(code)));
+}
+
+__device__ __forceinline__ uint16_t finalize_scale_bits(float maximum) {
+  return __half_as_ushort(__float2half_rn(fmaxf(maximum / 127.0f, 0x1p-20f)));
+}
+
+// Codes of 8 FP16 values (two dwords of 4 codes).
+__device__ __forceinline__ v2u codes8(const _Float16 (&x)[8], float scale) {
+  uint32_t w[2] = {0u, 0u};
+#pragma unroll
+  for (int e = 0; e < 8; ++e)
+    w[e >> 2] |= symmetric_code_byte(static_cast<float>(x[e]) / scale) << (8 * (e & 3));
+  return v2u{w[0], w[1]};
+}
+
+// Finalize of one completed page from the FP16 pass's registers: k[j] holds
+// K row m16, dims 32j + 8kg .. +7; v[r] holds V row 4kg + r, dims 8*m16 .. +7
+// (the whole 16 x 128 block of this wave's head).  Writes the INT8 codes and
+// the two page scales of code page ``page`` of ``request``.
+__device__ void finalize_page(const DecodeArgs& a, int request, int page, int kv, int lane,
+                              const v8h (&k)[4], const v4u (&v)[4]) {
+  const int m16 = lane & 15;
+  const int kg = lane >> 4;
+  _Float16 kx[4][8], vx[4][8];
+  float kmax = 0.0f, vmax = 0.0f;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const v8h kb = k[j];
+    const v8h vb = __builtin_bit_cast(v8h, v[j]);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      kx[j][e] = kb[e];
+      vx[j][e] = vb[e];
+      kmax = fmaxf(kmax, fabsf(static_cast<float>(kx[j][e])));
+      vmax = fmaxf(vmax, fabsf(static_cast<float>(vx[j][e])));
+    }
+  }
+  const uint16_t k_bits = finalize_scale_bits(wave_max(kmax));
+  const uint16_t v_bits = finalize_scale_bits(wave_max(vmax));
+  const float k_scale = half_bits_to_float(k_bits);
+  const float v_scale = half_bits_to_float(v_bits);
+  const int hkv = a.num_kv_heads;
+  const int64_t row_stride = static_cast<int64_t>(hkv) * kHeadDim;
+  const int64_t code_page = static_cast<int64_t>(request) * a.code_pages_per_request + page;
+  int8_t* kc = a.finalize_k_codes + (code_page * kPageSize + m16) * row_stride + kv * kHeadDim + 8 * kg;
+  int8_t* vc = a.finalize_v_codes + (code_page * kPageSize + 4 * kg) * row_stride + kv * kHeadDim +
+               8 * m16;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    *reinterpret_cast<v2u*>(kc + 32 * j) = codes8(kx[j], k_scale);
+    *reinterpret_cast<v2u*>(vc + j * row_stride) = codes8(vx[j], v_scale);
+  }
+  if (lane == 0) {
+    a.finalize_k_scale[code_page * hkv + kv] = k_bits;
+    a.finalize_v_scale[code_page * hkv + kv] = v_bits;
+  }
+}
+
 __device__ __forceinline__ void fp16_pages(const DecodeArgs& a, int request, const uint16_t* kpages,
                                            const uint16_t* vpages, const int32_t* indices,
                                            int begin, int end, int last_page, int last_len,
@@ -550,6 +625,13 @@ __device__ __forceinline__ void fp16_pages(const DecodeArgs& a, int request, con
     v4f acc = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
     for (int j = 0; j < 4; ++j) acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(qa[j], cur.k[j], acc, 0, 0, 0);
+    if (a.finalize_positions != nullptr && slot == last_slot) {
+      // the step's token completed this (the segment's last) page
+      const int position = a.finalize_positions[request * a.finalize_position_stride];
+      if (position >= 0 && position % kPageSize == kPageSize - 1 &&
+          position / kPageSize < a.code_pages_per_request)
+        finalize_page(a, request, position / kPageSize, kv, lane, cur.k, cur.v);
+    }
     const int lim = slot == last_slot ? last_len : kPageSize;
     if (lim < kPageSize) {
       // rows past the last token: zero V so that p = 0 cannot meet a NaN or
@@ -1236,13 +1318,20 @@ PartialViews partial_views(const pg_decode_plan_t* plan, void* workspace) {
 
 namespace {
 
+// Decode-step finalize of pg_decode_run_finalize (positions null: none).
+struct FinalizeSpec {
+  const int32_t* positions = nullptr;
+  int position_stride = 0;
+  int code_pages_per_request = 0;
+};
+
 int32_t launch_partial(const pg_decode_plan_t* plan, const void* query,
                        int64_t query_batch_stride, const void* k_cache, const void* v_cache,
                        const void* k_scale, const void* v_scale, const int32_t* indices,
                        const int32_t* last_page_len, const void* tail_k, const void* tail_v,
                        const int32_t* tail_indices, const int32_t* tail_last_len, float sm_scale,
                        void* workspace, void* stream, void* start_event, void* stop_event,
-                       const int32_t* old_kv_len = nullptr) {
+                       const int32_t* old_kv_len = nullptr, FinalizeSpec finalize = {}) {
   clear_error();
   if (!plan || !query || !workspace) return fail(PG_ERROR_INVALID_ARGUMENT, "null run argument");
   if ((plan->primary_kind == PG_KV_HETEROGENEOUS) != (old_kv_len != nullptr))
@@ -1290,6 +1379,19 @@ int32_t launch_partial(const pg_decode_plan_t* plan, const void* query,
     return fail(PG_ERROR_INVALID_ARGUMENT, "plan has an invalid waves_per_block");
   a.max_items = std::max(1, plan->max_items_per_request);
   a.sm_scale_log2 = sm_scale * 1.4426950408889634f;
+  if (finalize.positions != nullptr) {
+    if (plan->primary_kind == PG_KV_FP16 || !k_cache || !v_cache || !k_scale || !v_scale)
+      return fail(PG_ERROR_INVALID_ARGUMENT, "the finalize writes into INT8 code pages and scales");
+    if (finalize.code_pages_per_request <= 0 || finalize.position_stride < 0)
+      return fail(PG_ERROR_INVALID_ARGUMENT, "finalize needs positive code pages per request");
+    a.finalize_positions = finalize.positions;
+    a.finalize_position_stride = finalize.position_stride;
+    a.code_pages_per_request = finalize.code_pages_per_request;
+    a.finalize_k_codes = static_cast<int8_t*>(const_cast<void*>(k_cache));
+    a.finalize_v_codes = static_cast<int8_t*>(const_cast<void*>(v_cache));
+    a.finalize_k_scale = static_cast<uint16_t*>(const_cast<void*>(k_scale));
+    a.finalize_v_scale = static_cast<uint16_t*>(const_cast<void*>(v_scale));
+  }
   if (plan->closed_form) {
     if (plan->batch_size != 1 || plan->cf_tail_items < 0 || plan->cf_tail_items > plan->num_items ||
         plan->cf_tail_pages < plan->cf_tail_items || plan->cf_tail_pages < 0 ||
@@ -1357,11 +1459,11 @@ int32_t run_decode(const pg_decode_plan_t* plan, const void* query, int64_t quer
                    const int32_t* tail_last_len, const void* value_center,
                    int64_t center_batch_stride, void* out, float* lse, float sm_scale,
                    void* workspace, void* stream, void* start_event, void* stop_event,
-                   const int32_t* old_kv_len = nullptr) {
+                   const int32_t* old_kv_len = nullptr, FinalizeSpec finalize = {}) {
   if (int32_t rc = launch_partial(plan, query, query_batch_stride, k_cache, v_cache, k_scale,
                                   v_scale, indices, last_page_len, tail_k, tail_v, tail_indices,
                                   tail_last_len, sm_scale, workspace, stream, start_event, nullptr,
-                                  old_kv_len))
+                                  old_kv_len, finalize))
     return rc;
   return launch_combine(plan, value_center, center_batch_stride, out, lse, workspace, stream,
                         stop_event);
@@ -1442,6 +1544,47 @@ extern "C" int32_t pg_decode_run_heterogeneous(
                     last_page_len, exact_k, exact_v, nullptr, nullptr, value_center,
                     center_batch_stride, out, lse, sm_scale, workspace, stream, nullptr, nullptr,
                     old_kv_len);
+}
+
+extern "C" int32_t pg_decode_run_finalize(
+    const pg_decode_plan_t* plan, const void* query, int64_t query_batch_stride,
+    const void* k_cache, const void* v_cache, const void* k_scale, const void* v_scale,
+    const int32_t* indices, const int32_t* last_page_len, const void* tail_k, const void* tail_v,
+    const int32_t* tail_indices, const int32_t* tail_last_len, const void* value_center,
+    int64_t center_batch_stride, void* out, float* lse, float sm_scale, void* workspace,
+    const int32_t* positions, int32_t position_stride, int32_t code_pages_per_request,
+    void* stream) {
+  clear_error();
+  if (!positions) return fail(PG_ERROR_INVALID_ARGUMENT, "finalize positions are required");
+  FinalizeSpec f;
+  f.positions = positions;
+  f.position_stride = position_stride;
+  f.code_pages_per_request = code_pages_per_request;
+  return run_decode(plan, query, query_batch_stride, k_cache, v_cache, k_scale, v_scale, indices,
+                    last_page_len, tail_k, tail_v, tail_indices, tail_last_len, value_center,
+                    center_batch_stride, out, lse, sm_scale, workspace, stream, nullptr, nullptr,
+                    nullptr, f);
+}
+
+extern "C" int32_t pg_decode_run_heterogeneous_finalize(
+    const pg_decode_plan_t* plan, const void* query, int64_t query_batch_stride,
+    const void* k_codes, const void* v_codes, const void* k_scale, const void* v_scale,
+    const void* exact_k, const void* exact_v, const int32_t* indices,
+    const int32_t* last_page_len, const int32_t* old_kv_len, const void* value_center,
+    int64_t center_batch_stride, void* out, float* lse, float sm_scale, void* workspace,
+    const int32_t* positions, int32_t position_stride, int32_t code_pages_per_request,
+    void* stream) {
+  clear_error();
+  if (!old_kv_len) return fail(PG_ERROR_INVALID_ARGUMENT, "old_kv_len is required");
+  if (!positions) return fail(PG_ERROR_INVALID_ARGUMENT, "finalize positions are required");
+  FinalizeSpec f;
+  f.positions = positions;
+  f.position_stride = position_stride;
+  f.code_pages_per_request = code_pages_per_request;
+  return run_decode(plan, query, query_batch_stride, k_codes, v_codes, k_scale, v_scale, indices,
+                    last_page_len, exact_k, exact_v, nullptr, nullptr, value_center,
+                    center_batch_stride, out, lse, sm_scale, workspace, stream, nullptr, nullptr,
+                    old_kv_len, f);
 }
 
 extern "C" int32_t pg_merge_state_in_place(void* v, float* s, const void* v_other,

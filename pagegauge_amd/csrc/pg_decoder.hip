@@ -9,7 +9,14 @@
 //   * SiLU(gate) * up of the fused gate/up projection -- epilogue: the
 //     workgroup that computes gate row i also computes up row i + n/2;
 //   * the residual add (FP16 output of the projection, then an FP16 add) --
-//     epilogue.
+//     epilogue;
+//   * for the QKV projection, the decode step's cache update
+//     (rope_append_page_gauge_dynamic / rope_append_fp16_dynamic of
+//     tests/page_gauge_append_extension.cu without its page finalize): each
+//     workgroup computes rows d and d + 64 of one head, rotates query and key
+//     rows, centers key and value rows and writes them into their ring slot
+//     -- epilogue.  The completed page's INT8 finalize runs in the decode's
+//     FP16 tail pass (pg_decode_run_finalize).
 //
 // The work is HBM-bound weight streaming (M = batch <= 4): every weight byte
 // is read once.  A workgroup (4 waves) owns a group of rows; the 512-element
@@ -33,7 +40,10 @@ constexpr int kGemvWaves = kGemvThreads / kWave;
 constexpr int kChunk = 512;          // elements per wave-wide 16-byte load
 constexpr int kUnroll = 4;           // chunks in flight per row (generic kernel)
 constexpr int kMaxBatch = 4;
-constexpr int kMaxBlocks = 2048;
+#ifndef PG_GEMV_MAX_BLOCKS
+#define PG_GEMV_MAX_BLOCKS 2048
+#endif
+constexpr int kMaxBlocks = PG_GEMV_MAX_BLOCKS;   // grid cap (grid-stride beyond it)
 constexpr size_t kMaxStagedBytes = 64 * 1024;   // generic kernel: input staged in LDS
 // Output rows per workgroup of the blocked kernels (k = 4096 with n <= 8192
 // or larger; k = 14336).  A SwiGLU workgroup loads twice as many rows.
@@ -46,6 +56,27 @@ constexpr size_t kMaxStagedBytes = 64 * 1024;   // generic kernel: input staged 
 #ifndef PG_GEMV_ROWS_14336
 #define PG_GEMV_ROWS_14336 2
 #endif
+
+// Cache update of a decode step, applied to the QKV projection's output.
+struct AppendArgs {
+  int query_heads;
+  int kv_heads;
+  const uint16_t* cosine;      // [rope_rows, 128] FP16
+  const uint16_t* sine;
+  int64_t rope_row_stride;
+  int rope_rows;
+  const int32_t* positions;    // device, positions[b * position_stride]
+  int position_stride;
+  uint16_t* rotated_query;     // [batch, query_heads, 128]
+  uint16_t* key_pages;         // FP16 pages [pages, 16, kv_heads, 128] or the exact ring
+  uint16_t* value_pages;
+  const uint16_t* key_center;  // [batch, kv_heads, 128] (stride center_batch_stride); null:
+  const uint16_t* value_center;//   plain FP16 pages, no centering
+  int64_t center_batch_stride;
+  int pages_per_request;       // FP16 pages, or exact ring pages (sink + tail) per request
+  int sink_pages;              // fixed prefix pages of the ring
+  int capacity_tokens;         // positions at or past it (or the RoPE table) are skipped
+};
 
 struct GemvArgs {
   const uint16_t* weight;      // [n, k] row-major FP16
@@ -63,6 +94,7 @@ struct GemvArgs {
   int out_rows;                // n, or n/2 with swiglu
   int k;
   int iterations;
+  AppendArgs append;
 };
 
 __device__ __forceinline__ float h2f(uint16_t b) { return half_bits_to_float(b); }
@@ -131,19 +163,119 @@ __device__ __forceinline__ void store_output(const GemvArgs& a, int b, int row, 
 
 // Weight row of the block's r-th loaded row: output rows row0.. (and, with
 // SwiGLU, the matching up rows n/2 + row0..); rows past the end are clamped
-// (loaded, never stored).
-template <int kR>
+// (loaded, never stored).  With the append epilogue the block's two rows are
+// dims d and d + 64 of one 128-row head, d = (row0 / 2) % 64.
+template <int kR, bool kRope>
 __device__ __forceinline__ int loaded_row(const GemvArgs& a, int row0, int r) {
+  if constexpr (kRope) {
+    const int pair = row0 / 2;
+    return (pair / 64) * kHeadDim + pair % 64 + 64 * r;
+  }
   const int out_row = min(row0 + (r % kR), a.out_rows - 1);
   return r < kR ? out_row : out_row + a.out_rows;
 }
 
-template <int kR, int kLoad, int kC>
+__device__ __forceinline__ _Float16 bits_h(uint16_t b) { return __builtin_bit_cast(_Float16, b); }
+
+// rn16(rn16(x*c) + rn16(partner*s)), the partner negated for the first half
+// (the rounding sequence of tests/page_gauge_append_extension.cu:154-160).
+__device__ __forceinline__ uint16_t rope_element(uint16_t x, uint16_t partner, uint16_t c,
+                                                 uint16_t s, bool flip) {
+#pragma clang fp contract(off)
+  if (flip) partner ^= 0x8000u;
+  const _Float16 primary = bits_h(x) * bits_h(c);
+  const _Float16 secondary = bits_h(partner) * bits_h(s);
+  return __builtin_bit_cast(uint16_t, static_cast<_Float16>(primary + secondary));
+}
+
+// fp16(float(a) - float(b))
+__device__ __forceinline__ uint16_t centered(uint16_t a, uint16_t b) {
+  return f2h(h2f(a) - h2f(b));
+}
+
+// Epilogue inputs of one (batch row, head pair), loaded at kernel start so
+// that their latency hides under the weight stream.
+struct AppendInputs {
+  int position;
+  bool valid;
+  uint16_t cos_lo, cos_hi, sin_lo, sin_hi, center_lo, center_hi;
+};
+
+__device__ __forceinline__ AppendInputs append_inputs(const GemvArgs& g, int b, int pair) {
+  const AppendArgs& a = g.append;
+  AppendInputs in{};
+  in.position = a.positions[b * a.position_stride];
+  in.valid = in.position >= 0 && in.position < a.capacity_tokens && in.position < a.rope_rows;
+  if (!in.valid) return in;
+  const int h = pair / 64;
+  const int d = pair % 64;
+  if (h < a.query_heads + a.kv_heads) {
+    const int64_t row = static_cast<int64_t>(in.position) * a.rope_row_stride;
+    in.cos_lo = a.cosine[row + d];
+    in.cos_hi = a.cosine[row + d + 64];
+    in.sin_lo = a.sine[row + d];
+    in.sin_hi = a.sine[row + d + 64];
+  }
+  if (h >= a.query_heads && a.key_center != nullptr) {
+    const bool value = h >= a.query_heads + a.kv_heads;
+    const int head = h - a.query_heads - (value ? a.kv_heads : 0);
+    const uint16_t* center = (value ? a.value_center : a.key_center) + b * a.center_batch_stride +
+                             head * kHeadDim;
+    in.center_lo = center[d];
+    in.center_hi = center[d + 64];
+  }
+  return in;
+}
+
+// Append epilogue for batch row b: y_lo / y_hi are dims d and d + 64 of
+// head h of the QKV output (query heads, then key heads, then value heads).
+__device__ void append_pair(const GemvArgs& g, int b, int pair, float y_lo, float y_hi,
+                            const AppendInputs& in) {
+  const AppendArgs& a = g.append;
+  if (!in.valid) return;
+  const int position = in.position;
+  const int h = pair / 64;
+  const int d = pair % 64;
+  uint16_t lo = f2h(y_lo);
+  uint16_t hi = f2h(y_hi);
+  if (h < a.query_heads + a.kv_heads) {
+    const uint16_t r_lo = rope_element(lo, hi, in.cos_lo, in.sin_lo, true);
+    const uint16_t r_hi = rope_element(hi, lo, in.cos_hi, in.sin_hi, false);
+    lo = r_lo;
+    hi = r_hi;
+  }
+  if (h < a.query_heads) {
+    uint16_t* q = a.rotated_query + (static_cast<int64_t>(b) * a.query_heads + h) * kHeadDim;
+    q[d] = lo;
+    q[d + 64] = hi;
+    return;
+  }
+  const bool value = h >= a.query_heads + a.kv_heads;
+  const int head = h - a.query_heads - (value ? a.kv_heads : 0);
+  const int page = position / kPageSize;
+  const int token = position % kPageSize;
+  int64_t physical;
+  if (a.key_center == nullptr) {
+    physical = static_cast<int64_t>(b) * a.pages_per_request + page;
+  } else {
+    const int tail_pages = a.pages_per_request - a.sink_pages;
+    const int local = page < a.sink_pages ? page : a.sink_pages + page % tail_pages;
+    physical = static_cast<int64_t>(b) * a.pages_per_request + local;
+    lo = centered(lo, in.center_lo);
+    hi = centered(hi, in.center_hi);
+  }
+  uint16_t* dst = (value ? a.value_pages : a.key_pages) +
+                  ((physical * kPageSize + token) * a.kv_heads + head) * kHeadDim;
+  dst[d] = lo;
+  dst[d + 64] = hi;
+}
+
+template <int kR, int kLoad, int kC, bool kRope>
 __device__ __forceinline__ void load_rows(const GemvArgs& a, int row0, int wave, int lane,
                                           v4u_t (&wr)[kLoad][kC]) {
 #pragma unroll
   for (int r = 0; r < kLoad; ++r) {
-    const int row = loaded_row<kR>(a, row0, r);
+    const int row = loaded_row<kR, kRope>(a, row0, r);
     const uint16_t* w = a.weight + static_cast<int64_t>(row) * a.k + (wave * kC) * kChunk + lane * 8;
 #pragma unroll
     for (int c = 0; c < kC; ++c)
@@ -153,9 +285,10 @@ __device__ __forceinline__ void load_rows(const GemvArgs& a, int row0, int wave,
 
 // Blocked kernel: k = 4 * kC * 512.  kR output rows per workgroup (2*kR
 // weight rows with SwiGLU); grid-stride over row groups when the grid is
-// capped.
-template <int kBatch, int kR, int kC, bool kSwiglu>
+// capped.  kRope: the append epilogue (kR = 2, rows d and d + 64 of a head).
+template <int kBatch, int kR, int kC, bool kSwiglu, bool kRope = false>
 __global__ __launch_bounds__(kGemvThreads) void decoder_gemv_kernel(GemvArgs a) {
+  static_assert(!kRope || (kR == 2 && !kSwiglu), "the append epilogue pairs two rows");
   constexpr int kLoad = kSwiglu ? 2 * kR : kR;
   __shared__ float partial[kGemvWaves][kBatch][kLoad];
   __shared__ float squares[kGemvWaves][kBatch];
@@ -163,7 +296,12 @@ __global__ __launch_bounds__(kGemvThreads) void decoder_gemv_kernel(GemvArgs a) 
   const int lane = threadIdx.x % kWave;
   v4u_t wr[kLoad][kC];
   int row0 = blockIdx.x * kR;
-  if (row0 < a.out_rows) load_rows<kR, kLoad, kC>(a, row0, wave, lane, wr);
+  if (row0 < a.out_rows) load_rows<kR, kLoad, kC, kRope>(a, row0, wave, lane, wr);
+  AppendInputs append_in{};
+  if constexpr (kRope) {
+    // one row pair per workgroup (no grid-stride iterations)
+    if (threadIdx.x < kBatch && row0 < a.out_rows) append_in = append_inputs(a, threadIdx.x, row0 / 2);
+  }
 
   // this wave's slice of the input, in registers
   v4u_t xv[kBatch][kC];
@@ -201,7 +339,7 @@ __global__ __launch_bounds__(kGemvThreads) void decoder_gemv_kernel(GemvArgs a) 
 
   for (int it = 0; it < a.iterations; ++it, row0 += gridDim.x * kR) {
     if (row0 >= a.out_rows) break;                         // uniform over the block
-    if (it > 0) load_rows<kR, kLoad, kC>(a, row0, wave, lane, wr);
+    if (it > 0) load_rows<kR, kLoad, kC, kRope>(a, row0, wave, lane, wr);
     float acc[kBatch][kLoad];
 #pragma unroll
     for (int b = 0; b < kBatch; ++b) {
@@ -225,7 +363,16 @@ __global__ __launch_bounds__(kGemvThreads) void decoder_gemv_kernel(GemvArgs a) 
       }
     }
     __syncthreads();
-    if (threadIdx.x < kBatch * kR) {
+    if (kRope && threadIdx.x < kBatch) {
+      const int b = threadIdx.x;
+      float y0 = 0.0f, y1 = 0.0f;
+#pragma unroll
+      for (int w = 0; w < kGemvWaves; ++w) {
+        y0 += partial[w][b][0];
+        y1 += partial[w][b][1];
+      }
+      append_pair(a, b, row0 / 2, y0, y1, append_in);
+    } else if (!kRope && threadIdx.x < kBatch * kR) {
       const int b = threadIdx.x / kR;
       const int r = threadIdx.x % kR;
       const int row = row0 + r;
@@ -360,6 +507,15 @@ int32_t launch_gemv(GemvArgs a, hipStream_t s) {
   return check_launch("decoder_gemv");
 }
 
+template <int kBatch>
+int32_t launch_qkv_append(GemvArgs a, hipStream_t s) {
+  const int64_t blocks = a.out_rows / 2;      // one row pair per workgroup
+  a.iterations = 1;
+  hipLaunchKernelGGL((decoder_gemv_kernel<kBatch, 2, 2, false, true>),
+                     dim3(static_cast<unsigned>(blocks)), dim3(kGemvThreads), 0, s, a);
+  return check_launch("decoder_qkv_rope_append");
+}
+
 }  // namespace
 }  // namespace pg
 
@@ -404,5 +560,70 @@ extern "C" int32_t pg_decoder_gemv(const void* weight, int32_t n, int32_t k, con
     case 2: return launch_gemv<2>(a, s);
     case 3: return launch_gemv<3>(a, s);
     default: return launch_gemv<4>(a, s);
+  }
+}
+
+extern "C" int32_t pg_decoder_qkv_rope_append(
+    const void* weight, int32_t k, const void* x, int64_t x_stride, int32_t batch,
+    const void* norm_weight, float eps, int32_t query_heads, int32_t kv_heads, const void* cosine,
+    const void* sine, int64_t rope_row_stride, int32_t rope_rows, const int32_t* positions,
+    int32_t position_stride, void* rotated_query, void* key_pages, void* value_pages,
+    const void* key_center, const void* value_center, int64_t center_batch_stride,
+    int32_t pages_per_request, int32_t sink_pages, int32_t capacity_tokens, void* stream) {
+  clear_error();
+  if (weight == nullptr || x == nullptr || cosine == nullptr || sine == nullptr ||
+      positions == nullptr || rotated_query == nullptr || key_pages == nullptr ||
+      value_pages == nullptr)
+    return fail(PG_ERROR_INVALID_ARGUMENT, "null tensor pointer");
+  if ((key_center == nullptr) != (value_center == nullptr))
+    return fail(PG_ERROR_INVALID_ARGUMENT, "key and value centers go together");
+  if (k != 8 * kChunk)
+    return fail(PG_ERROR_UNSUPPORTED, "the QKV append projection takes a 4096-wide input");
+  if (batch < 1 || batch > kMaxBatch)
+    return fail(PG_ERROR_UNSUPPORTED, "decoder projections take a batch of 1 to 4 rows");
+  if (query_heads <= 0 || kv_heads <= 0 || query_heads % kv_heads)
+    return fail(PG_ERROR_INVALID_ARGUMENT, "query heads must be a positive multiple of KV heads");
+  if (x_stride < k || x_stride % 8 || rope_row_stride < kHeadDim || rope_rows <= 0 ||
+      position_stride < 0)
+    return fail(PG_ERROR_INVALID_ARGUMENT, "row strides must cover the rows (input stride a multiple of 8)");
+  if (pages_per_request <= 0 || sink_pages < 0 ||
+      (key_center != nullptr && sink_pages >= pages_per_request) || capacity_tokens < 0)
+    return fail(PG_ERROR_INVALID_ARGUMENT, "invalid page geometry");
+  if (key_center != nullptr && center_batch_stride < static_cast<int64_t>(kv_heads) * kHeadDim &&
+      batch > 1)
+    return fail(PG_ERROR_INVALID_ARGUMENT, "center batch stride must cover the KV heads");
+  GemvArgs a{};
+  a.weight = static_cast<const uint16_t*>(weight);
+  a.x = static_cast<const uint16_t*>(x);
+  a.x_stride = x_stride;
+  a.norm_weight = static_cast<const uint16_t*>(norm_weight);
+  a.eps = eps;
+  a.n = (query_heads + 2 * kv_heads) * kHeadDim;
+  a.out_rows = a.n;
+  a.k = k;
+  AppendArgs& p = a.append;
+  p.query_heads = query_heads;
+  p.kv_heads = kv_heads;
+  p.cosine = static_cast<const uint16_t*>(cosine);
+  p.sine = static_cast<const uint16_t*>(sine);
+  p.rope_row_stride = rope_row_stride;
+  p.rope_rows = rope_rows;
+  p.positions = positions;
+  p.position_stride = position_stride;
+  p.rotated_query = static_cast<uint16_t*>(rotated_query);
+  p.key_pages = static_cast<uint16_t*>(key_pages);
+  p.value_pages = static_cast<uint16_t*>(value_pages);
+  p.key_center = static_cast<const uint16_t*>(key_center);
+  p.value_center = static_cast<const uint16_t*>(value_center);
+  p.center_batch_stride = center_batch_stride;
+  p.pages_per_request = pages_per_request;
+  p.sink_pages = sink_pages;
+  p.capacity_tokens = capacity_tokens;
+  hipStream_t s = as_stream(stream);
+  switch (batch) {
+    case 1: return launch_qkv_append<1>(a, s);
+    case 2: return launch_qkv_append<2>(a, s);
+    case 3: return launch_qkv_append<3>(a, s);
+    default: return launch_qkv_append<4>(a, s);
   }
 }

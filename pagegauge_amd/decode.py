@@ -80,6 +80,18 @@ def _check_index(t: torch.Tensor, name: str) -> None:
         raise ValueError(f"{name} must be a contiguous CUDA int32 tensor")
 
 
+def _finalize_args(finalize, batch: int, code_pages: int):
+    """(positions, position stride, code pages per request) of a finalize."""
+    positions, per_request = finalize
+    _check_index(positions, "finalize positions")
+    if positions.numel() not in (1, batch):
+        raise ValueError("finalize positions must be one per request or one shared")
+    per_request = int(per_request)
+    if per_request <= 0 or per_request * batch > code_pages:
+        raise ValueError("code pages per request exceed the code pool")
+    return positions, (1 if positions.numel() == batch and batch > 1 else 0), per_request
+
+
 class _Planned:
     """Holds a C plan, the device index tensors it refers to and the workspace."""
 
@@ -382,7 +394,12 @@ class PageGaugeSegmentedDecode:
         return self._state.num_items
 
     def run(self, q, codes, k_page_scale, v_page_scale, exact_cache, value_center=None,
-            sm_scale: Optional[float] = None, out=None, lse=None, return_lse: bool = False):
+            sm_scale: Optional[float] = None, out=None, lse=None, return_lse: bool = False,
+            finalize: Optional[tuple] = None):
+        """``finalize=(positions, code_pages_per_request)``: also finalize the
+        page that the token at ``positions`` (device int32, one per request,
+        or one shared) completed, into ``codes`` and the page scales
+        (``pg_decode_run_finalize``; the cache update then ran without it)."""
         if not self._state.planned:
             raise RuntimeError("plan() must be called before run()")
         k_codes, v_codes = codes
@@ -409,12 +426,18 @@ class PageGaugeSegmentedDecode:
         if return_lse and lse is None:
             lse = torch.empty(q.size(0), q.size(1), device=q.device, dtype=torch.float32)
         scale = self._sm_scale if sm_scale is None else sm_scale
-        _capi.call("pg_decode_run", ctypes.byref(self._state.plan), q.data_ptr(), q.stride(0),
-                   k_codes.data_ptr(), v_codes.data_ptr(), k_page_scale.data_ptr(),
-                   v_page_scale.data_ptr(), self._old[0].data_ptr(), self._old[1].data_ptr(),
-                   exact_k.data_ptr(), exact_v.data_ptr(), self._tail[0].data_ptr(),
-                   self._tail[1].data_ptr(), _ptr(value_center), center_stride, out.data_ptr(),
-                   _ptr(lse), float(scale), self._state.workspace.data_ptr(), _stream())
+        args = (ctypes.byref(self._state.plan), q.data_ptr(), q.stride(0), k_codes.data_ptr(),
+                v_codes.data_ptr(), k_page_scale.data_ptr(), v_page_scale.data_ptr(),
+                self._old[0].data_ptr(), self._old[1].data_ptr(), exact_k.data_ptr(),
+                exact_v.data_ptr(), self._tail[0].data_ptr(), self._tail[1].data_ptr(),
+                _ptr(value_center), center_stride, out.data_ptr(), _ptr(lse), float(scale),
+                self._state.workspace.data_ptr())
+        if finalize is None:
+            _capi.call("pg_decode_run", *args, _stream())
+        else:
+            positions, stride, code_pages = _finalize_args(finalize, self._batch, k_codes.size(0))
+            _capi.call("pg_decode_run_finalize", *args, positions.data_ptr(), stride, code_pages,
+                       _stream())
         return (out, lse) if return_lse else out
 
     def bind(self, q, codes, k_page_scale, v_page_scale, exact_cache, value_center=None,
@@ -526,7 +549,10 @@ class HeterogeneousDecodeWrapper:
 
     def run(self, q, paged_kv_cache, k_page_scale, v_page_scale, exact_k_cache, exact_v_cache,
             old_kv_len, value_center, sm_scale: Optional[float] = None, out=None, lse=None,
-            return_lse: bool = False, **_unused):
+            return_lse: bool = False, finalize: Optional[tuple] = None, **_unused):
+        """``finalize=(positions, code_pages_per_request)``: also finalize the
+        page that the token at ``positions`` (device int32, one per request,
+        or one shared) completed (``pg_decode_run_heterogeneous_finalize``)."""
         if not self._state.planned:
             raise RuntimeError("plan() must be called before run()")
         old_k, old_v = paged_kv_cache
@@ -548,12 +574,18 @@ class HeterogeneousDecodeWrapper:
         if return_lse and lse is None:
             lse = torch.empty(q.size(0), q.size(1), device=q.device, dtype=torch.float32)
         scale = self._sm_scale if sm_scale is None else float(sm_scale)
-        _capi.call("pg_decode_run_heterogeneous", ctypes.byref(self._state.plan), q.data_ptr(),
-                   q.stride(0), old_k.data_ptr(), old_v.data_ptr(), k_page_scale.data_ptr(),
-                   v_page_scale.data_ptr(), exact_k_cache.data_ptr(), exact_v_cache.data_ptr(),
-                   self._indices.data_ptr(), self._last_page_len.data_ptr(), old_kv_len.data_ptr(),
-                   value_center.data_ptr(), self._num_kv_heads * DIM, out.data_ptr(), _ptr(lse),
-                   scale, self._state.workspace.data_ptr(), _stream())
+        args = (ctypes.byref(self._state.plan), q.data_ptr(), q.stride(0), old_k.data_ptr(),
+                old_v.data_ptr(), k_page_scale.data_ptr(), v_page_scale.data_ptr(),
+                exact_k_cache.data_ptr(), exact_v_cache.data_ptr(), self._indices.data_ptr(),
+                self._last_page_len.data_ptr(), old_kv_len.data_ptr(), value_center.data_ptr(),
+                self._num_kv_heads * DIM, out.data_ptr(), _ptr(lse), scale,
+                self._state.workspace.data_ptr())
+        if finalize is None:
+            _capi.call("pg_decode_run_heterogeneous", *args, _stream())
+        else:
+            positions, stride, code_pages = _finalize_args(finalize, self._batch, old_k.size(0))
+            _capi.call("pg_decode_run_heterogeneous_finalize", *args, positions.data_ptr(), stride,
+                       code_pages, _stream())
         return (out, lse) if return_lse else out
 
 

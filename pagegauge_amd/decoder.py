@@ -154,6 +154,46 @@ def projection(weight: torch.Tensor, x: torch.Tensor, out: torch.Tensor, *,
     return out
 
 
+def qkv_rope_append(weight: torch.Tensor, x: torch.Tensor, *, norm_weight: torch.Tensor,
+                    eps: float, query_heads: int, kv_heads: int, cos: torch.Tensor,
+                    sin: torch.Tensor, positions: torch.Tensor, rotated_query: torch.Tensor,
+                    key_pages: torch.Tensor, value_pages: torch.Tensor,
+                    key_center: Optional[torch.Tensor], value_center: Optional[torch.Tensor],
+                    pages_per_request: int, sink_pages: int, capacity_tokens: int) -> None:
+    """The QKV projection fused with the decode step's cache update
+    (``pg_decoder_qkv_rope_append``): RMSNorm, QKV rows, RoPE of query and
+    key, and the (centered, with ``key_center``) append of key and value at
+    ``positions`` (device int32, one shared or one per row) -- bit-identical to
+    ``projection`` followed by ``rope_append_page_gauge_dynamic`` /
+    ``rope_append_fp16_dynamic``, except that the PageGauge page finalize is
+    left to the decode (``finalize=`` of its run)."""
+    from . import _capi
+
+    batch, k = int(x.shape[0]), int(x.shape[1])
+    rows = (query_heads + 2 * kv_heads) * DIM
+    if (weight.dtype != torch.float16 or not weight.is_contiguous()
+            or tuple(weight.shape) != (rows, k)):
+        raise ValueError("QKV weights must be contiguous FP16 [(Hq + 2 Hkv) * 128, K]")
+    if x.dtype != torch.float16 or x.stride(1) != 1:
+        raise ValueError("projection input must be FP16 [B, K] rows")
+    for t, name in ((cos, "cos"), (sin, "sin"), (rotated_query, "rotated_query"),
+                    (key_pages, "key_pages"), (value_pages, "value_pages")):
+        if t.dtype != torch.float16 or not t.is_contiguous():
+            raise ValueError(f"{name} must be contiguous FP16")
+    if positions.dtype != torch.int32 or positions.numel() not in (1, batch):
+        raise ValueError("positions must be int32, one shared or one per row")
+    stride = 1 if positions.numel() == batch and batch > 1 else 0
+    center_stride = 0 if key_center is None else key_center.stride(0)
+    _capi.call("pg_decoder_qkv_rope_append", weight.data_ptr(), k, x.data_ptr(), x.stride(0),
+               batch, norm_weight.data_ptr(), float(eps), query_heads, kv_heads, cos.data_ptr(),
+               sin.data_ptr(), cos.stride(0), int(cos.shape[0]), positions.data_ptr(), stride,
+               rotated_query.data_ptr(), key_pages.data_ptr(), value_pages.data_ptr(),
+               None if key_center is None else key_center.data_ptr(),
+               None if value_center is None else value_center.data_ptr(), center_stride,
+               int(pages_per_request), int(sink_pages), int(capacity_tokens),
+               torch.cuda.current_stream().cuda_stream)
+
+
 def rms_norm(x: torch.Tensor, weight: torch.Tensor, eps: float) -> torch.Tensor:
     """MistralRMSNorm: float32 statistics, FP16 product with the weight."""
     x32 = x.float()
@@ -404,7 +444,7 @@ class PageGaugeDecoder:
                  rope_cos: torch.Tensor, rope_sin: torch.Tensor, exact_tail: int = 256,
                  split_pages: int = 0, batch_size: int = 1, exact_sink_pages: int = 0,
                  workspace_bytes: int = 128 * 1024 * 1024, fused: Optional[bool] = None,
-                 tail_attention: str = "segmented") -> None:
+                 tail_attention: str = "segmented", fused_append: Optional[bool] = None) -> None:
         if backend not in ("page_gauge", "fp16"):
             raise ValueError(f"unknown backend {backend}")
         if tail_attention not in ("segmented", "heterogeneous"):
@@ -500,6 +540,12 @@ class PageGaugeDecoder:
         if self.fused and not ok:
             raise ValueError("fused projections need batch <= 4 and widths that are multiples "
                              "of 512 (4096 / 14336, or batch * width <= 32768)")
+        # the QKV projection carries the cache update (pg_decoder_qkv_rope_append;
+        # the PageGauge page finalize then runs in the decode's FP16 pass)
+        append_ok = self.fused and cfg.hidden == 4096
+        self.fused_append = append_ok if fused_append is None else fused_append
+        if self.fused_append and not append_ok:
+            raise ValueError("the fused cache update needs fused projections and hidden 4096")
         self._hidden = torch.empty(batch_size, cfg.hidden, device=device, dtype=torch.float16)
         self._qkv = torch.empty(batch_size, cfg.qkv_width, device=device, dtype=torch.float16)
         self._activation = torch.empty(batch_size, cfg.intermediate, device=device,
@@ -596,6 +642,27 @@ class PageGaugeDecoder:
             c.exact_value[layer], c.key_codes[layer], c.value_codes[layer], c.key_scales[layer],
             c.value_scales[layer], self.exact_sink_pages)
 
+    def _qkv_append(self, layer: int) -> None:
+        """QKV projection + RoPE + cache append in one launch."""
+        cfg = self.config
+        w = self.weights.layers[layer]
+        c = self.cache
+        common = dict(norm_weight=w["input_norm"], eps=cfg.rms_eps, query_heads=cfg.q_heads,
+                      kv_heads=cfg.kv_heads, cos=self.rope_cos, sin=self.rope_sin,
+                      positions=self.device_position, rotated_query=self.rotated_query)
+        if self.backend == "fp16":
+            qkv_rope_append(w["qkv"], self._hidden, key_pages=c.key[layer],
+                            value_pages=c.value[layer], key_center=None, value_center=None,
+                            pages_per_request=c.pages_per_request, sink_pages=0,
+                            capacity_tokens=c.pages_per_request * PAGE, **common)
+            return
+        qkv_rope_append(w["qkv"], self._hidden, key_pages=c.exact_key[layer],
+                        value_pages=c.exact_value[layer], key_center=c.key_center[layer],
+                        value_center=c.value_center[layer],
+                        pages_per_request=c.exact_storage_pages_per_request,
+                        sink_pages=self.exact_sink_pages,
+                        capacity_tokens=c.pages_per_request * PAGE, **common)
+
     def attention(self, layer: int) -> torch.Tensor:
         out = self.attention_output[layer]
         if self.backend == "fp16":
@@ -603,26 +670,34 @@ class PageGaugeDecoder:
                                                         self.cache.value[layer]), out=out)
         c = self.cache
         value_center = c.value_center[layer]
+        # with the fused cache update, the decode finalizes a completed page
+        finalize = (self.device_position, c.pages_per_request) if self.fused_append else None
         if self.tail_attention == "heterogeneous":
             return self.decode.run(self.rotated_query, (c.key_codes[layer], c.value_codes[layer]),
                                    c.key_scales[layer], c.value_scales[layer], c.exact_key[layer],
-                                   c.exact_value[layer], self.old_kv_len, value_center, out=out)
+                                   c.exact_value[layer], self.old_kv_len, value_center, out=out,
+                                   finalize=finalize)
         return self.decode.run(self.rotated_query, (c.key_codes[layer], c.value_codes[layer]),
                                c.key_scales[layer], c.value_scales[layer],
                                (c.exact_key[layer], c.exact_value[layer]),
-                               value_center=value_center, out=out)
+                               value_center=value_center, out=out, finalize=finalize)
 
     def _layer_fused(self, layer: int) -> None:
-        """One layer on ``self._hidden`` in place: 4 projection launches + K2 + K1."""
+        """One layer on ``self._hidden`` in place: 4 projection launches (the
+        QKV one carrying the cache update) + K1, or with ``fused_append`` off,
+        4 projections + K2 + K1."""
         cfg = self.config
         w = self.weights.layers[layer]
         b = self.batch_size
-        qkv = projection(w["qkv"], self._hidden, self._qkv, norm_weight=w["input_norm"],
-                         eps=cfg.rms_eps)
         qw, kw = cfg.q_heads * DIM, cfg.kv_heads * DIM
-        self._append(layer, qkv[:, :qw].view(b, cfg.q_heads, DIM),
-                     qkv[:, qw:qw + kw].view(b, cfg.kv_heads, DIM),
-                     qkv[:, qw + kw:].view(b, cfg.kv_heads, DIM))
+        if self.fused_append:
+            self._qkv_append(layer)
+        else:
+            qkv = projection(w["qkv"], self._hidden, self._qkv, norm_weight=w["input_norm"],
+                             eps=cfg.rms_eps)
+            self._append(layer, qkv[:, :qw].view(b, cfg.q_heads, DIM),
+                         qkv[:, qw:qw + kw].view(b, cfg.kv_heads, DIM),
+                         qkv[:, qw + kw:].view(b, cfg.kv_heads, DIM))
         attended = self.attention(layer)
         projection(w["o"], attended.view(b, qw), self._hidden, residual=self._hidden)
         projection(w["gate_up"], self._hidden, self._activation, norm_weight=w["post_norm"],

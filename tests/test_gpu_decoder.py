@@ -196,3 +196,45 @@ def test_decoder_requires_the_hip_library(setup, monkeypatch):
         _fresh(dec, decoders["page_gauge"])
     with pytest.raises(_capi.LibraryMissingError):
         decoders["page_gauge"].step(tokens[:1], PROMPT)     # its first plan needs the library
+
+
+def _cache_tensors(cache):
+    return {k: v for k, v in vars(cache).items() if isinstance(v, torch.Tensor)}
+
+
+@pytest.mark.parametrize("backend,tail,sink", [("page_gauge", "segmented", 0),
+                                               ("page_gauge", "heterogeneous", 0),
+                                               ("fp16", "segmented", 0),
+                                               ("page_gauge", "segmented", 2)])
+def test_fused_cache_update_is_bitwise_the_separate_update(setup, backend, tail, sink):
+    """The QKV projection carrying RoPE + append (pg_decoder_qkv_rope_append)
+    and the decode's finalize of a completed page (pg_decode_run_finalize)
+    leave the caches and logits bit-identical to the projection followed by
+    the K2 launch, across a page completion (position 527)."""
+    dec, weights, first, decoders, tokens = setup
+    if sink:
+        gen = torch.Generator().manual_seed(20260850)
+        prompt = torch.randint(0, weights.config.vocab, (PROMPT,), generator=gen)
+        _, _, built = dec.build_decoders(weights, prompt, STEPS + 1, backends=("page_gauge",),
+                                         exact_sink_pages=sink)
+        base = built["page_gauge"]
+    else:
+        base = decoders[backend]
+
+    def make(fused_append):
+        return dec.PageGaugeDecoder(weights, base.cache.clone(), backend, base.max_pages * 16,
+                                    base.rope_cos, base.rope_sin, base.exact_tail_pages * 16,
+                                    exact_sink_pages=base.exact_sink_pages, tail_attention=tail,
+                                    fused_append=fused_append)
+
+    fused, separate = make(True), make(False)
+    assert fused.fused_append and not separate.fused_append
+    for i in range(STEPS):
+        a = fused.step(tokens[i:i + 1], PROMPT + i).clone()
+        b = separate.step(tokens[i:i + 1], PROMPT + i)
+        assert torch.equal(a, b), f"logits differ at step {i}"
+    for name, value in _cache_tensors(fused.cache).items():
+        assert torch.equal(value, _cache_tensors(separate.cache)[name]), name
+    if backend == "page_gauge":
+        # the page completed at position 527 (logical page 32) was finalized
+        assert fused.cache.key_scales[:, 32].abs().min() > 0

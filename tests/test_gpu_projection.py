@@ -142,3 +142,63 @@ def test_fused_decoder_step_matches_torch_op_step(cuda):
         assert float((a - b).abs().max()) <= 0.02 * max(1.0, scale), i
         assert float(F.cosine_similarity(a, b, dim=-1).min()) > 0.9999
         token = b.argmax(-1)
+
+
+@pytest.mark.parametrize("centered,batch", [(True, 2), (False, 2), (True, 1)])
+def test_qkv_rope_append_is_projection_then_cache_update(cuda, centered, batch):
+    """pg_decoder_qkv_rope_append against pg_decoder_gemv followed by the K2
+    per-request-positions launch, bit for bit: rotated queries and the ring
+    (or FP16 page) rows; row 1 sits past the cache capacity and writes
+    nothing.  Positions stay off page ends, where K2 also finalizes."""
+    from pagegauge_amd.decoder import projection, qkv_rope_append, rope_tables
+    from pagegauge_amd.runtime import load_append_extension
+
+    print(f"qkv append centered={centered} batch={batch}", flush=True)
+    ext = load_append_extension()
+    gen = torch.Generator().manual_seed(77 + batch + 2 * centered)
+    hq, hkv, k, pages, sink = 32, 8, 4096, 6, 1
+    w = _rand(gen, (hq + 2 * hkv) * 128, k, scale=0.02).to(cuda)
+    x = _rand(gen, batch, k).to(cuda)
+    g = _rand(gen, k, scale=0.5).to(cuda)
+    cos, sin = (t.to(cuda) for t in rope_tables(pages * 16, 1.0e6))
+    positions = torch.tensor([37, 10_000][:batch], dtype=torch.int32, device=cuda)
+    kc = _rand(gen, batch, hkv, 128, scale=0.1).to(cuda)
+    vc = _rand(gen, batch, hkv, 128, scale=0.1).to(cuda)
+    ring = 4 if centered else pages
+    shape = (batch * ring, 16, hkv, 128)
+    bufs = [dict(q=torch.zeros(batch, hq, 128, device=cuda, dtype=torch.float16),
+                 k=torch.zeros(shape, device=cuda, dtype=torch.float16),
+                 v=torch.zeros(shape, device=cuda, dtype=torch.float16)) for _ in range(2)]
+    fused, ref = bufs
+    qkv_rope_append(w, x, norm_weight=g, eps=1e-5, query_heads=hq, kv_heads=hkv, cos=cos, sin=sin,
+                    positions=positions, rotated_query=fused["q"], key_pages=fused["k"],
+                    value_pages=fused["v"], key_center=kc if centered else None,
+                    value_center=vc if centered else None, pages_per_request=ring,
+                    sink_pages=sink if centered else 0, capacity_tokens=pages * 16)
+    qkv = torch.empty(batch, (hq + 2 * hkv) * 128, device=cuda, dtype=torch.float16)
+    projection(w, x, qkv, norm_weight=g, eps=1e-5)
+    q = qkv[:, :hq * 128].reshape(batch, hq, 128)
+    kk = qkv[:, hq * 128:(hq + hkv) * 128].reshape(batch, hkv, 128)
+    vv = qkv[:, (hq + hkv) * 128:].reshape(batch, hkv, 128)
+    if centered:
+        codes = torch.zeros(batch * pages, 16, hkv, 128, device=cuda, dtype=torch.int8)
+        scales = torch.zeros(batch * pages, hkv, device=cuda, dtype=torch.float16)
+        ext.rope_append_page_gauge_positions(q.contiguous(), kk.contiguous(), vv.contiguous(),
+                                             cos, sin, positions, kc, vc, ref["q"], ref["k"],
+                                             ref["v"], codes, codes.clone(), scales,
+                                             scales.clone(), sink)
+    else:
+        for b in range(batch):
+            p = int(positions[b])
+            if p >= pages * 16:
+                continue
+            ext.rope_append_fp16_dynamic(q[b:b + 1].contiguous(), kk[b:b + 1].contiguous(),
+                                         vv[b:b + 1].contiguous(), cos, sin, positions[b:b + 1],
+                                         ref["q"][b:b + 1], ref["k"][b * pages:(b + 1) * pages],
+                                         ref["v"][b * pages:(b + 1) * pages])
+    torch.cuda.synchronize()
+    for name in ("q", "k", "v"):
+        assert torch.equal(fused[name], ref[name]), name
+    assert fused["k"].abs().sum() > 0
+    if batch > 1:
+        assert not fused["q"][1].any()              # out-of-capacity row: no writes
