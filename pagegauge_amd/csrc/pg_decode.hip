@@ -1099,6 +1099,7 @@ int32_t build_plan(const int32_t* host_indptr, const int32_t* host_last_page_len
       segments.push_back({b, primary_kind, 0, host_indptr[b], host_indptr[b + 1], 1.0});
   }
   std::vector<int> chunks(segments.size(), 0);
+  bool medium = false;
   if (split_pages > 0) {
     // fixed split (FlashInfer fixed_split_size semantics): pages per work item
     if (tail_split_pages <= 0)
@@ -1129,15 +1130,22 @@ int32_t build_plan(const int32_t* host_indptr, const int32_t* host_last_page_len
     };
     double lo = 1e-3, hi = 1.0;
     for (const Segment& sg : segments) hi += (sg.end - sg.begin) * sg.weight;
-    // Measured on MI355X (B1/49K split sweep): once the batch has a few
-    // thousand pages, 16-page chunks beat finer ones because each work
-    // item pays a fixed start-up (page-table load, then the first group);
-    // smaller problems use chunks down to one PV group for parallelism.
-    lo = hi >= 12.0 * static_cast<double>(target) ? kLargeBatchMinChunk : 1e-3;
-    if (count_for(hi, nullptr) <= target) {
+    // Measured on MI355X (B=1 sweeps from 4K to 49K tokens):
+    // * large (>= 12 pages per CU): 16-page chunks beat finer ones, because
+    //   each work item pays a fixed start-up (page ids, then the first
+    //   group), on up to one 8-wave workgroup per CU;
+    // * medium (3..12 pages per CU): about 7/16 of the CUs in items, each
+    //   split over two half-height workgroups (one wave per SIMD), so every
+    //   wave pipelines 2..6 groups (16K: 12.8 against 13.9 us);
+    // * small: chunks down to one PV group for parallelism.
+    const double per_cu = hi / static_cast<double>(target);
+    medium = per_cu >= 3.0 && per_cu < 12.0;
+    const int64_t item_target = medium ? std::max<int64_t>(1, target * 7 / 16) : target;
+    lo = per_cu >= 12.0 ? kLargeBatchMinChunk : 1e-3;
+    if (count_for(hi, nullptr) <= item_target) {
       for (int iter = 0; iter < 64; ++iter) {
         const double mid = 0.5 * (lo + hi);
-        if (count_for(mid, nullptr) <= target) hi = mid; else lo = mid;
+        if (count_for(mid, nullptr) <= item_target) hi = mid; else lo = mid;
       }
     }
     count_for(hi, &chunks);
@@ -1195,6 +1203,13 @@ int32_t build_plan(const int32_t* host_indptr, const int32_t* host_last_page_len
   p.max_items_per_request = max_per_request;
   p.waves_per_block = waves_per_block_for(num_kv_heads, static_cast<int64_t>(items.size()),
                                           num_cus > 0 ? num_cus : 256);
+  if (medium) {
+    // two workgroups per item: the largest allowed divisor of Hkv below Hkv
+    int w = kMaxWavesPerBlock;
+    while (w > 1 && num_kv_heads % w) w >>= 1;
+    if (w == num_kv_heads && w > 1) w >>= 1;
+    p.waves_per_block = w;
+  }
   // One request: describe the items in closed form when the formula gives
   // exactly the table (the kernel then skips the work-item load).
   if (batch_size == 1 && !items.empty()) {
