@@ -1131,17 +1131,18 @@ int32_t build_plan(const int32_t* host_indptr, const int32_t* host_last_page_len
     double lo = 1e-3, hi = 1.0;
     for (const Segment& sg : segments) hi += (sg.end - sg.begin) * sg.weight;
     // Measured on MI355X (B=1 sweeps from 4K to 49K tokens):
-    // * large (>= 12 pages per CU): 16-page chunks beat finer ones, because
+    // * large (>= 16 pages per CU): 16-page chunks beat finer ones, because
     //   each work item pays a fixed start-up (page ids, then the first
     //   group), on up to one 8-wave workgroup per CU;
-    // * medium (3..12 pages per CU): about 7/16 of the CUs in items, each
+    // * medium (3..16 pages per CU): about 7/16 of the CUs in items, each
     //   split over two half-height workgroups (one wave per SIMD), so every
-    //   wave pipelines 2..6 groups (16K: 12.8 against 13.9 us);
+    //   wave pipelines 2..7 groups (16K: 12.6 against 13.9 us; 49K: the same
+    //   partial kernel time as 193 items, and a cheaper combine);
     // * small: chunks down to one PV group for parallelism.
     const double per_cu = hi / static_cast<double>(target);
-    medium = per_cu >= 3.0 && per_cu < 12.0;
+    medium = per_cu >= 3.0 && per_cu < 16.0;
     const int64_t item_target = medium ? std::max<int64_t>(1, target * 7 / 16) : target;
-    lo = per_cu >= 12.0 ? kLargeBatchMinChunk : 1e-3;
+    lo = per_cu >= 16.0 ? kLargeBatchMinChunk : 1e-3;
     if (count_for(hi, nullptr) <= item_target) {
       for (int iter = 0; iter < 64; ++iter) {
         const double mid = 0.5 * (lo + hi);

@@ -54,6 +54,26 @@ def test_balanced_plan_covers_every_page_once(old, tail):
     assert plan.max_items_per_request == max(int(ptr[b + 1] - ptr[b]) for b in range(len(old)))
 
 
+@pytest.mark.parametrize("tokens,items,waves", [(4096, 64, 2), (8192, 128, 4), (16400, 112, 4),
+                                                (49152, 112, 4)])
+def test_one_request_plan_regimes(tokens, items, waves):
+    """Small problems: chunks down to one PV group; medium (3..16 weighted
+    pages per CU, B1/49K included): 7/16 of the CUs in items, each over two
+    half-height workgroups."""
+    old = tokens // 16 - 16
+    plan, got, _ = plan_work_items([0, old], [16], [0, 16], [16])
+    assert (plan.num_items, plan.waves_per_block) == (items, waves)
+    assert plan.num_items * (8 // plan.waves_per_block) <= 256      # one wave of workgroups
+
+
+def test_b8_ragged_plans_stay_large():
+    lengths = workloads.ragged_lengths(workloads.VALIDATION_SEEDS[0])
+    old = [(n - 256) // 16 for n in lengths]
+    plan, items, _ = plan_work_items(_indptr(old), [16] * 8, _indptr([16] * 8), [16] * 8)
+    assert plan.waves_per_block == 8 and plan.num_items <= 256
+    assert (items[:, 4] - items[:, 3])[items[:, 2] == 0].min() >= 16
+
+
 def test_b1_49k_plan_uses_sixteen_page_chunks_within_one_wave():
     plan, items, _ = plan_work_items([0, 3056], [16], [0, 16], [16])
     sizes = (items[:, 4] - items[:, 3]).numpy()
