@@ -587,7 +587,8 @@ extern "C" int32_t pg_decoder_qkv_rope_append(
       position_stride < 0)
     return fail(PG_ERROR_INVALID_ARGUMENT, "row strides must cover the rows (input stride a multiple of 8)");
   if (pages_per_request <= 0 || sink_pages < 0 ||
-      (key_center != nullptr && sink_pages >= pages_per_request) || capacity_tokens < 0)
+      (key_center != nullptr && sink_pages >= pages_per_request) || capacity_tokens < 0 ||
+      (key_center == nullptr && capacity_tokens > pages_per_request * kPageSize))
     return fail(PG_ERROR_INVALID_ARGUMENT, "invalid page geometry");
   if (key_center != nullptr && center_batch_stride < static_cast<int64_t>(kv_heads) * kHeadDim &&
       batch > 1)

@@ -182,8 +182,32 @@ def qkv_rope_append(weight: torch.Tensor, x: torch.Tensor, *, norm_weight: torch
             raise ValueError(f"{name} must be contiguous FP16")
     if positions.dtype != torch.int32 or positions.numel() not in (1, batch):
         raise ValueError("positions must be int32, one shared or one per row")
+    tensors = (weight, x, norm_weight, cos, sin, positions, rotated_query, key_pages, value_pages)
+    if not all(t.is_cuda and t.device == weight.device for t in tensors):
+        raise ValueError("all tensors must be on the weights' CUDA device")
+    if norm_weight.dtype != torch.float16 or norm_weight.numel() != k:
+        raise ValueError("norm weight must be FP16 [K]")
+    if cos.shape != sin.shape or cos.dim() != 2 or cos.shape[1] != DIM:
+        raise ValueError("RoPE tables must be matching [positions, 128] tensors")
+    if tuple(rotated_query.shape) != (batch, query_heads, DIM):
+        raise ValueError("rotated_query must be [B, Hq, 128]")
+    if (key_pages.shape != value_pages.shape or key_pages.dim() != 4
+            or tuple(key_pages.shape[1:]) != (PAGE, kv_heads, DIM)
+            or key_pages.shape[0] < batch * pages_per_request):
+        raise ValueError("key/value pages must be [>= B * pages_per_request, 16, Hkv, 128]")
+    if key_center is None:
+        if value_center is not None or capacity_tokens > pages_per_request * PAGE:
+            raise ValueError("FP16 pages: no centers, capacity within pages_per_request pages")
+    else:
+        for center in (key_center, value_center):
+            if (center is None or center.dtype != torch.float16 or not center.is_contiguous()
+                    or tuple(center.shape[-2:]) != (kv_heads, DIM)
+                    or center.numel() != batch * kv_heads * DIM):
+                raise ValueError("centers must be contiguous FP16 [B, Hkv, 128]")
+        if not 0 <= sink_pages < pages_per_request:
+            raise ValueError("the exact ring needs at least one tail page after the sink")
     stride = 1 if positions.numel() == batch and batch > 1 else 0
-    center_stride = 0 if key_center is None else key_center.stride(0)
+    center_stride = 0 if key_center is None else kv_heads * DIM
     _capi.call("pg_decoder_qkv_rope_append", weight.data_ptr(), k, x.data_ptr(), x.stride(0),
                batch, norm_weight.data_ptr(), float(eps), query_heads, kv_heads, cos.data_ptr(),
                sin.data_ptr(), cos.stride(0), int(cos.shape[0]), positions.data_ptr(), stride,

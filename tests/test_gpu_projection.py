@@ -202,3 +202,34 @@ def test_qkv_rope_append_is_projection_then_cache_update(cuda, centered, batch):
     assert fused["k"].abs().sum() > 0
     if batch > 1:
         assert not fused["q"][1].any()              # out-of-capacity row: no writes
+
+
+def test_qkv_rope_append_rejects_bad_geometry(cuda):
+    """Host checks keep every write of the fused cache update inside its
+    tensors (the kernel itself trusts them)."""
+    from pagegauge_amd.decoder import qkv_rope_append, rope_tables
+
+    hq, hkv, k = 32, 8, 4096
+    w = torch.zeros((hq + 2 * hkv) * 128, k, device=cuda, dtype=torch.float16)
+    x = torch.zeros(1, k, device=cuda, dtype=torch.float16)
+    g = torch.ones(k, device=cuda, dtype=torch.float16)
+    cos, sin = (t.to(cuda) for t in rope_tables(64, 1.0e6))
+    pos = torch.zeros(1, dtype=torch.int32, device=cuda)
+    rq = torch.empty(1, hq, 128, device=cuda, dtype=torch.float16)
+    pages = torch.zeros(4, 16, hkv, 128, device=cuda, dtype=torch.float16)
+    kc = torch.zeros(1, hkv, 128, device=cuda, dtype=torch.float16)
+    ok = dict(norm_weight=g, eps=1e-5, query_heads=hq, kv_heads=hkv, cos=cos, sin=sin,
+              positions=pos, rotated_query=rq, key_pages=pages, value_pages=pages.clone(),
+              key_center=kc, value_center=kc.clone(), pages_per_request=4, sink_pages=1,
+              capacity_tokens=64)
+    qkv_rope_append(w, x, **ok)
+    for change, message in ((dict(pages_per_request=5), "pages_per_request"),
+                            (dict(sink_pages=4), "tail page"),
+                            (dict(key_center=None, value_center=None, capacity_tokens=65),
+                             "capacity"),
+                            (dict(rotated_query=rq[:, :16]), "rotated_query"),
+                            (dict(key_center=kc[:, :4]), "centers"),
+                            (dict(positions=torch.zeros(2, dtype=torch.int32, device=cuda)),
+                             "positions")):
+        with pytest.raises(ValueError, match=message):
+            qkv_rope_append(w, x, **{**ok, **change})
