@@ -107,6 +107,7 @@ PROTOTYPES = {
     "pg_decoder_qkv_rope_append": (_i32, [_p, _i32, _p, _i64, _i32, _p, _f32, _i32, _i32, _p, _p,
                                           _i64, _i32, _p, _i32, _p, _p, _p, _p, _p, _i64, _i32,
                                           _i32, _i32, _p]),
+    "pg_argmax_f32": (_i32, [_p, _i32, _i32, _i64, _p, _p]),
     "pg_merge_state_in_place": (_i32, [_p, _p, _p, _p, _p, _i32, _i32, _i32, _p]),
     "pg_exact_tail_merge_center": (_i32, [_p, _p, _p, _p, _p, _p, _p, _p, _i64, _i32, _i32, _i32,
                                           _i32, _f32, _p]),

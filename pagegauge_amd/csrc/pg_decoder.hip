@@ -507,6 +507,54 @@ int32_t launch_gemv(GemvArgs a, hipStream_t s) {
   return check_launch("decoder_gemv");
 }
 
+// Greedy token selection: torch.argmax over each row of float32 logits
+// (the first index of the maximum; NaN counts as the largest value).
+constexpr int kArgmaxThreads = 1024;
+
+__device__ __forceinline__ bool argmax_better(float v, int i, float bv, int bi) {
+  const bool nan = v != v, bnan = bv != bv;
+  if (nan != bnan) return nan;
+  if (!nan && v != bv) return v > bv;
+  return i < bi;
+}
+
+__global__ __launch_bounds__(kArgmaxThreads) void argmax_kernel(const float* x, int n,
+                                                                 int64_t row_stride,
+                                                                 int64_t* out) {
+  __shared__ float best_v[kArgmaxThreads / kWave];
+  __shared__ int best_i[kArgmaxThreads / kWave];
+  const float* row = x + blockIdx.x * row_stride;
+  float bv = -__builtin_huge_valf();
+  int bi = n;                                     // any real index beats it on ties
+  const int vec = (reinterpret_cast<uintptr_t>(row) % 16 == 0) ? n / 4 : 0;
+  for (int j = threadIdx.x; j < vec; j += kArgmaxThreads) {
+    const float4 v = reinterpret_cast<const float4*>(row)[j];
+    const float e[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+    for (int t = 0; t < 4; ++t)
+      if (argmax_better(e[t], 4 * j + t, bv, bi)) { bv = e[t]; bi = 4 * j + t; }
+  }
+  for (int i = 4 * vec + threadIdx.x; i < n; i += kArgmaxThreads)
+    if (argmax_better(row[i], i, bv, bi)) { bv = row[i]; bi = i; }
+#pragma unroll
+  for (int off = kWave / 2; off > 0; off >>= 1) {
+    const float ov = __shfl_xor(bv, off, kWave);
+    const int oi = __shfl_xor(bi, off, kWave);
+    if (argmax_better(ov, oi, bv, bi)) { bv = ov; bi = oi; }
+  }
+  const int wave = threadIdx.x / kWave;
+  if (threadIdx.x % kWave == 0) {
+    best_v[wave] = bv;
+    best_i[wave] = bi;
+  }
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    for (int w = 1; w < kArgmaxThreads / kWave; ++w)
+      if (argmax_better(best_v[w], best_i[w], bv, bi)) { bv = best_v[w]; bi = best_i[w]; }
+    out[blockIdx.x] = bi < n ? bi : 0;
+  }
+}
+
 template <int kBatch>
 int32_t launch_qkv_append(GemvArgs a, hipStream_t s) {
   const int64_t blocks = a.out_rows / 2;      // one row pair per workgroup
@@ -627,4 +675,15 @@ extern "C" int32_t pg_decoder_qkv_rope_append(
     case 3: return launch_qkv_append<3>(a, s);
     default: return launch_qkv_append<4>(a, s);
   }
+}
+
+extern "C" int32_t pg_argmax_f32(const float* x, int32_t rows, int32_t n, int64_t row_stride,
+                                 int64_t* out, void* stream) {
+  clear_error();
+  if (x == nullptr || out == nullptr) return fail(PG_ERROR_INVALID_ARGUMENT, "null tensor pointer");
+  if (rows < 1 || n < 1 || row_stride < n)
+    return fail(PG_ERROR_INVALID_ARGUMENT, "argmax needs rows of at least one element");
+  hipLaunchKernelGGL(argmax_kernel, dim3(rows), dim3(kArgmaxThreads), 0, as_stream(stream), x, n,
+                     row_stride, out);
+  return check_launch("argmax");
 }

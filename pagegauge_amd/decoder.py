@@ -218,6 +218,21 @@ def qkv_rope_append(weight: torch.Tensor, x: torch.Tensor, *, norm_weight: torch
                torch.cuda.current_stream().cuda_stream)
 
 
+def argmax_rows(x: torch.Tensor, out: torch.Tensor) -> torch.Tensor:
+    """``torch.argmax(x, dim=-1, out=out)`` for float32 logits [B, V] in one
+    HIP launch (``pg_argmax_f32``): the first index of the maximum, NaN
+    counting as the largest value."""
+    from . import _capi
+
+    if x.dtype != torch.float32 or x.dim() != 2 or x.stride(1) != 1 or not x.is_cuda:
+        raise ValueError("argmax input must be CUDA float32 [B, V] rows")
+    if out.dtype != torch.int64 or out.numel() != x.shape[0] or not out.is_contiguous():
+        raise ValueError("argmax output must be contiguous int64 [B]")
+    _capi.call("pg_argmax_f32", x.data_ptr(), int(x.shape[0]), int(x.shape[1]), x.stride(0),
+               out.data_ptr(), torch.cuda.current_stream().cuda_stream)
+    return out
+
+
 def rms_norm(x: torch.Tensor, weight: torch.Tensor, eps: float) -> torch.Tensor:
     """MistralRMSNorm: float32 statistics, FP16 product with the weight."""
     x32 = x.float()
@@ -804,7 +819,10 @@ class PageGaugeDecoder:
         with torch.cuda.graph(graph):
             logits = self._body(token)
             self.graph_logits.copy_(logits)
-            torch.argmax(self.graph_logits, dim=-1, out=self.graph_next)
+            if self.fused:
+                argmax_rows(self.graph_logits, self.graph_next)
+            else:
+                torch.argmax(self.graph_logits, dim=-1, out=self.graph_next)
         self.graph_bank[self.plan_signature()] = graph
 
     def drop_graphs(self) -> None:

@@ -233,3 +233,31 @@ def test_qkv_rope_append_rejects_bad_geometry(cuda):
                              "positions")):
         with pytest.raises(ValueError, match=message):
             qkv_rope_append(w, x, **{**ok, **change})
+
+
+@pytest.mark.parametrize("rows,n,stride", [(1, 32768, 32768), (4, 32768, 32768), (3, 1001, 1003),
+                                           (2, 5, 8)])
+def test_argmax_rows_is_torch_argmax(cuda, rows, n, stride):
+    """pg_argmax_f32 against torch.argmax: random rows, a tie planted at two
+    positions (the first wins), a NaN (it wins), an all -inf row (index 0),
+    rows that are not 16-byte aligned."""
+    from pagegauge_amd.decoder import argmax_rows
+
+    print(f"argmax rows={rows} n={n} stride={stride}", flush=True)
+    gen = torch.Generator().manual_seed(rows * 7 + n)
+    base = torch.randn(rows, stride, generator=gen)
+    if rows > 1:
+        top = float(base[1, :n].max()) + 1.0
+        base[1, n // 3] = top
+        base[1, n - 1] = top                      # later tie: the first index wins
+    if rows > 2:
+        base[2, n // 2] = float("nan")
+        base[2, 0] = float("inf")
+    x = base.to(cuda)[:, :n]
+    if rows == 4:
+        x[3] = -float("inf")
+    out = torch.empty(rows, device=cuda, dtype=torch.int64)
+    argmax_rows(x, out)
+    want = torch.argmax(x, dim=-1)
+    torch.cuda.synchronize()
+    assert torch.equal(out, want), (out.tolist(), want.tolist())
