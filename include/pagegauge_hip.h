@@ -487,9 +487,11 @@ int32_t pg_decoder_qkv_rope_append(const void* weight, int32_t k, const void* x,
 
 /* Greedy token selection of the decode loop: out[r] = argmax of row r of
  * x [rows, row_stride] float32 over its first n elements, as
- * torch.argmax(logits, dim=-1) in the reference decoder's greedy step
- * (scripts/benchmark_page_gauge_transformer.py:3706-3860): the first index of
- * the maximum, NaN counting as the largest value.  One workgroup per row. */
+ * logits.argmax(dim=-1) in the reference decoder (the step's "gpu_argmax",
+ * scripts/benchmark_page_gauge_transformer.py:2602 and :2650; the top-1
+ * comparison at :3880; scripts/probe_certified_hierarchical_attention.py:249):
+ * the first index of the maximum, NaN counting as the largest value.  One
+ * workgroup per row. */
 int32_t pg_argmax_f32(const float* x, int32_t rows, int32_t n, int64_t row_stride, int64_t* out,
                       void* stream);
 
