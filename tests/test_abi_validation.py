@@ -1,0 +1,108 @@
+"""Host-side argument checks of the C ABI, run without a GPU.
+
+Every case below fails a check that the entry point makes before it touches
+the HIP runtime, so the call returns an error code and a message and launches
+nothing.  The messages of the cache-update checks are the ones the
+reference's tests assert ("must be nonnegative", "at least one tail-ring
+page", "logical cache capacity": tests/test_page_gauge_append_extension.py
+:520-585).  Cases pass stand-in (non-null, never dereferenced) pointers to
+get past the null checks, so the module is skipped wherever a GPU is
+visible: a check that regressed there must not turn into a launch on such an
+address.
+"""
+
+from __future__ import annotations
+
+import ctypes
+
+import pytest
+import torch
+
+from pagegauge_amd import _capi
+
+pytestmark = pytest.mark.skipif(torch.cuda.is_available(),
+                                reason="host-only checks: stand-in pointers are never launched")
+
+FAKE = 0x1000          # stand-in device address (a failing check returns before any use)
+
+
+def _call(name, *args):
+    rc = getattr(_capi.library(), name)(*args)
+    return rc, _capi.last_error()
+
+
+def _rope_append_page_gauge(**over):
+    a = dict(query=FAKE, key=FAKE, value=FAKE, cosine=FAKE, sine=FAKE, key_center=FAKE,
+             value_center=FAKE, center_batch_stride=8 * 128, rotated_query=FAKE,
+             exact_key=FAKE, exact_value=FAKE, key_codes=FAKE, value_codes=FAKE,
+             key_scales=FAKE, value_scales=FAKE, qbs=32 * 128, kbs=8 * 128, vbs=8 * 128,
+             batch=1, qh=32, kvh=8, exact_pages=16, sink=0, code_pages=64, position=100,
+             device_position=None, rope_row_stride=128, rope_rows=0, stream=None)
+    a.update(over)
+    return _call("pg_rope_append_page_gauge", *a.values())
+
+
+@pytest.mark.parametrize("over,code,message", [
+    (dict(batch=0), 1, "batch sizes must match and be positive"),
+    (dict(kvh=0), 1, "head counts must be positive"),
+    (dict(key_codes=None), 1, "null tensor pointer"),
+    (dict(sink=-1), 1, "must be nonnegative"),
+    (dict(exact_pages=2, sink=2), 1, "at least one tail-ring page"),
+    (dict(exact_pages=20, sink=5, code_pages=5), 1, "logical cache capacity"),
+    (dict(position=-1), 1, "position must be non-negative"),
+    (dict(position=64 * 16), 1, "exceeds the per-request PageGauge cache capacity"),
+    (dict(device_position=FAKE, rope_rows=0), 1, "dynamic RoPE tables"),
+])
+def test_rope_append_page_gauge_rejects(over, code, message):
+    rc, text = _rope_append_page_gauge(**over)
+    assert rc == code
+    assert message in text
+
+
+def _gemv(**over):
+    a = dict(weight=FAKE, n=4096, k=4096, x=FAKE, x_stride=4096, batch=1, norm=None,
+             eps=ctypes.c_float(1e-5), swiglu=0, residual=None, residual_stride=0, out=FAKE,
+             out_stride=4096, out_f32=0, stream=None)
+    a.update(over)
+    return _call("pg_decoder_gemv", *a.values())
+
+
+@pytest.mark.parametrize("over,code,message", [
+    (dict(weight=None), 1, "null tensor pointer"),
+    (dict(k=4000), 1, "multiple of 512"),
+    (dict(batch=5), 3, "batch of 1 to 4 rows"),
+    (dict(swiglu=1, n=4095), 1, "even n"),
+    (dict(x_stride=4100), 1, "row strides must cover the rows"),
+    (dict(out_stride=100), 1, "row strides must cover the rows"),
+])
+def test_decoder_gemv_rejects(over, code, message):
+    rc, text = _gemv(**over)
+    assert rc == code
+    assert message in text
+
+
+@pytest.mark.parametrize("args,message", [
+    ((None, 1, 10, 10, FAKE, None), "null tensor pointer"),
+    ((FAKE, 1, 0, 10, FAKE, None), "at least one element"),
+])
+def test_argmax_rejects(args, message):
+    rc, text = _call("pg_argmax_f32", *args)
+    assert rc == 1
+    assert message in text
+
+
+def test_decode_run_rejects_a_null_plan():
+    args = [None] * len(_capi.PROTOTYPES["pg_decode_run"][1])
+    args[17] = ctypes.c_float(0.088)         # sm_scale
+    args[2] = 0
+    args[14] = 0
+    rc, text = _call("pg_decode_run", *args)
+    assert rc == 1
+    assert "null run argument" in text
+
+
+def test_errors_do_not_leak_into_the_next_call():
+    rc, text = _gemv(weight=None)
+    assert rc == 1 and text
+    rc, text = _call("pg_argmax_f32", FAKE, 1, 0, 10, FAKE, None)
+    assert "at least one element" in text and "null" not in text
