@@ -510,6 +510,7 @@ int32_t launch_gemv(GemvArgs a, hipStream_t s) {
 // Greedy token selection: torch.argmax over each row of float32 logits
 // (the first index of the maximum; NaN counts as the largest value).
 constexpr int kArgmaxThreads = 1024;
+constexpr int kArgmaxUnroll = 8;     // float4 loads in flight per thread
 
 __device__ __forceinline__ bool argmax_better(float v, int i, float bv, int bi) {
   const bool nan = v != v, bnan = bv != bv;
@@ -527,12 +528,25 @@ __global__ __launch_bounds__(kArgmaxThreads) void argmax_kernel(const float* x, 
   float bv = -__builtin_huge_valf();
   int bi = n;                                     // any real index beats it on ties
   const int vec = (reinterpret_cast<uintptr_t>(row) % 16 == 0) ? n / 4 : 0;
-  for (int j = threadIdx.x; j < vec; j += kArgmaxThreads) {
-    const float4 v = reinterpret_cast<const float4*>(row)[j];
-    const float e[4] = {v.x, v.y, v.z, v.w};
+  // kArgmaxUnroll float4 loads per thread are issued before any is compared
+  // (a 32768-entry row is one such round); the selection is a total order,
+  // so the visiting order does not change the result
+  for (int base = 0; base < vec; base += kArgmaxThreads * kArgmaxUnroll) {
+    float4 v[kArgmaxUnroll];
 #pragma unroll
-    for (int t = 0; t < 4; ++t)
-      if (argmax_better(e[t], 4 * j + t, bv, bi)) { bv = e[t]; bi = 4 * j + t; }
+    for (int u = 0; u < kArgmaxUnroll; ++u) {
+      const int j = base + u * kArgmaxThreads + threadIdx.x;
+      v[u] = j < vec ? reinterpret_cast<const float4*>(row)[j] : make_float4(0.f, 0.f, 0.f, 0.f);
+    }
+#pragma unroll
+    for (int u = 0; u < kArgmaxUnroll; ++u) {
+      const int j = base + u * kArgmaxThreads + threadIdx.x;
+      if (j >= vec) continue;
+      const float e[4] = {v[u].x, v[u].y, v[u].z, v[u].w};
+#pragma unroll
+      for (int t = 0; t < 4; ++t)
+        if (argmax_better(e[t], 4 * j + t, bv, bi)) { bv = e[t]; bi = 4 * j + t; }
+    }
   }
   for (int i = 4 * vec + threadIdx.x; i < n; i += kArgmaxThreads)
     if (argmax_better(row[i], i, bv, bi)) { bv = row[i]; bi = i; }

@@ -843,6 +843,9 @@ class PageGaugeDecoder:
             logits = self.step(token, position)
             if use_graphs and self.plan_signature() in self.graph_bank:
                 token = self.graph_next.clone()
+            elif self.fused:
+                token = argmax_rows(logits, torch.empty(self.batch_size, dtype=torch.int64,
+                                                        device=logits.device))
             else:
                 token = logits.argmax(dim=-1)
             tokens.append(token)
