@@ -101,6 +101,7 @@ class _Planned:
         self.workspace = workspace
         self.plan = _capi.DecodePlan()
         self.planned = False
+        self.generation = 0     # advances with every plan written into ``self.plan``
 
     def make_plan(self, host_indptr, host_last, primary_kind, host_tail_indptr, host_tail_last,
                   num_qo_heads, num_kv_heads, head_dim, page_size, split_pages, tail_split_pages,
@@ -116,6 +117,7 @@ class _Planned:
             self.workspace.numel(), ctypes.byref(self.plan), _stream())
         _capi.check(rc, "decode plan")
         self.planned = True
+        self.generation += 1
 
     @property
     def split_pages(self) -> int:
@@ -170,14 +172,19 @@ class BoundDecode:
     the combine kernels), ``partial()`` / ``combine()`` the two kernels
     separately, and ``timed(start, stop)`` the call with two timing events
     stamped by its first and last kernel dispatches.  No tensor validation
-    happens here; the bound tensors must stay alive and keep their storage.
-    ``stream`` is a raw hipStream_t handle (default: the current stream when
-    ``bind`` was called)."""
+    happens here; the object holds references to the tensors it was bound to
+    (their storage must not be resized or swapped), and it is valid until its
+    wrapper plans again: a call after a new ``plan()`` raises RuntimeError,
+    since the plan and workspace then describe other tables.  ``stream`` is a
+    raw hipStream_t handle (default: the current stream when ``bind`` was
+    called)."""
 
     def __init__(self, state: "_Planned", partial_args: tuple, combine_args: tuple,
-                 stream: int) -> None:
+                 stream: int, keep: tuple = ()) -> None:
         lib = _capi.library()
         self._state = state
+        self._generation = state.generation
+        self._keep = keep
         self._plan_ref = ctypes.byref(state.plan)
         self._partial = lib.pg_decode_run_partial
         self._partial_timed = lib.pg_decode_run_partial_timed
@@ -191,7 +198,12 @@ class BoundDecode:
         self._run_args = (self._plan_ref, *partial_args[:-1], *combine_args, partial_args[-1], ws,
                           stream)
 
+    def _check_plan(self) -> None:
+        if self._state.generation != self._generation:
+            raise RuntimeError("the decode was planned again after bind(); bind it again")
+
     def partial(self) -> None:
+        self._check_plan()
         rc = self._partial(*self._partial_args)
         if rc:
             _capi.check(rc, "decode partial")
@@ -201,21 +213,25 @@ class BoundDecode:
         (raw hipEvent_t handles, e.g. ``torch.cuda.Event(enable_timing=True)``
         ``.cuda_event`` after one ``record()``): their elapsed time is the
         kernel's duration without the launch gap."""
+        self._check_plan()
         rc = self._partial_timed(*self._partial_args, start_event, stop_event)
         if rc:
             _capi.check(rc, "decode partial")
 
     def combine(self) -> None:
+        self._check_plan()
         rc = self._combine(*self._combine_args)
         if rc:
             _capi.check(rc, "decode combine")
 
     def timed(self, start_event: int, stop_event: int) -> None:
+        self._check_plan()
         rc = self._run_timed(*self._run_args, start_event, stop_event)
         if rc:
             _capi.check(rc, "decode run")
 
     def __call__(self) -> None:
+        self._check_plan()
         rc = self._run(*self._run_args)
         if rc:
             _capi.check(rc, "decode run")
@@ -330,7 +346,10 @@ class BatchDecodeWithPagedKVCacheWrapper:
                    _ptr(k_page_scale), _ptr(v_page_scale), self._indices.data_ptr(),
                    self._last_page_len.data_ptr(), None, None, None, None, float(scale))
         combine = (None, 0, out.data_ptr(), _ptr(lse))
-        return BoundDecode(self._state, partial, combine, _stream() if stream is None else stream)
+        keep = (q, k_cache, v_cache, k_page_scale, v_page_scale, self._indices,
+                self._last_page_len, out, lse)
+        return BoundDecode(self._state, partial, combine, _stream() if stream is None else stream,
+                           keep)
 
 
 def make_page_gauge_wrapper(flashinfer_module, workspace: torch.Tensor, **wrapper_kwargs):
@@ -457,7 +476,10 @@ class PageGaugeSegmentedDecode:
                    self._old[1].data_ptr(), exact_k.data_ptr(), exact_v.data_ptr(),
                    self._tail[0].data_ptr(), self._tail[1].data_ptr(), float(scale))
         combine = (_ptr(value_center), center_stride, out.data_ptr(), _ptr(lse))
-        return BoundDecode(self._state, partial, combine, _stream() if stream is None else stream)
+        keep = (q, k_codes, v_codes, k_page_scale, v_page_scale, exact_k, exact_v, *self._old,
+                *self._tail, value_center, out, lse)
+        return BoundDecode(self._state, partial, combine, _stream() if stream is None else stream,
+                           keep)
 
 
 def validate_heterogeneous_run_inputs(query, old_k_cache, old_v_cache, k_page_scale, v_page_scale,

@@ -280,3 +280,30 @@ def test_bound_timed_call_equals_plain_call(cuda, workspace):
         outs.append((cpu(out), cpu(lse)))
     assert np.array_equal(outs[0][0].view(np.uint16), outs[1][0].view(np.uint16))
     assert np.array_equal(outs[0][1].view(np.uint32), outs[1][1].view(np.uint32))
+
+
+def test_bound_decode_refuses_to_run_after_a_new_plan(cuda, workspace):
+    """A bound call carries the pointers of the tables it was bound to; once
+    its wrapper plans other tables into the workspace it must not launch."""
+    from pagegauge_amd import decode, workloads
+
+    w = workloads.build_decode_workload([4096], seed=20260842, device=cuda)
+    w2 = workloads.build_decode_workload([2048, 1024], seed=20260843, device=cuda)
+    dec = decode.PageGaugeSegmentedDecode(workspace)
+    dec.plan(w.old_indptr, w.old_indices, w.old_last_page_len, w.tail_indptr, w.tail_indices,
+             w.tail_last_page_len)
+    out = torch.empty_like(w.query)
+    bound = dec.bind(w.query, (w.k_codes, w.v_codes), w.k_scale, w.v_scale, (w.tail_k, w.tail_v),
+                     w.value_center, out=out)
+    bound()
+    dec.plan(w2.old_indptr, w2.old_indices, w2.old_last_page_len, w2.tail_indptr,
+             w2.tail_indices, w2.tail_last_page_len)
+    for call in (bound, bound.partial, bound.combine):
+        with pytest.raises(RuntimeError, match="planned again"):
+            call()
+    out2 = torch.empty_like(w2.query)
+    dec.bind(w2.query, (w2.k_codes, w2.v_codes), w2.k_scale, w2.v_scale, (w2.tail_k, w2.tail_v),
+             w2.value_center, out=out2)()
+    torch.cuda.synchronize()
+    ref_out, _, _ = oracle_decode(w2)
+    assert max_abs(out2, ref_out) <= OUT_TOL
