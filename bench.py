@@ -218,6 +218,74 @@ def decode_config(torch, decode, w, scrub, samples: int):
     }
 
 
+# The reference paper's isolated-attention microbenchmark on RTX 5090
+# (paper/mlsys2027/main.tex:140-156): B=4, 20,481-token contexts, mean latency
+# over 120 repeats with 256 MiB cache scrubs.
+PAPER_B4_20K_RTX5090_US = {"segmented": 132.20, "heterogeneous": 143.06, "fp16": 220.75}
+
+
+def paper_b4_20k(torch, decode, workloads, device, scrub, samples: int):
+    """The paper's B4 x 20K isolated-attention shape on this GPU: four
+    requests of 20480 tokens (1264 INT8 + 16 FP16 pages each; the paper's
+    20,481st token would add one row to a 1281st page), each call cold after
+    the 1 GiB read scrub.  Segmented call (partial + combine), heterogeneous
+    one-table call (the same pages through one unified table per request)
+    and the FP16 same-way kernel over an all-FP16 copy; mean and p50 of the
+    whole call, beside the paper's RTX 5090 means."""
+    w = workloads.build_decode_workload([20480] * 4, workloads.VALIDATION_SEEDS[0], device=device,
+                                        with_fp16_copy=True)
+    out = torch.empty_like(w.query)
+    lse = torch.empty(w.batch, 32, dtype=torch.float32, device=device)
+    bounds = {}
+    seg = decode.PageGaugeSegmentedDecode(torch.empty(64 << 20, dtype=torch.uint8, device=device))
+    seg.plan(w.old_indptr, w.old_indices, w.old_last_page_len, w.tail_indptr, w.tail_indices,
+             w.tail_last_page_len)
+    bounds["segmented"] = seg.bind(w.query, (w.k_codes, w.v_codes), w.k_scale, w.v_scale,
+                                   (w.tail_k, w.tail_v), w.value_center, out=out, lse=lse)
+    # one unified table per request: its INT8 pages, then its FP16 ring pages
+    old_ptr, tail_ptr = w.old_indptr.tolist(), w.tail_indptr.tolist()
+    old_idx, tail_idx = w.old_indices.cpu(), w.tail_indices.cpu()
+    rows, indptr, old_len = [], [0], []
+    for b in range(w.batch):
+        rows += [old_idx[old_ptr[b]:old_ptr[b + 1]], tail_idx[tail_ptr[b]:tail_ptr[b + 1]]]
+        indptr.append(indptr[-1] + old_ptr[b + 1] - old_ptr[b] + tail_ptr[b + 1] - tail_ptr[b])
+        old_len.append(16 * (old_ptr[b + 1] - old_ptr[b]))
+    unified = torch.cat(rows).to(device)
+    old_kv_len = torch.tensor(old_len, dtype=torch.int32, device=device)
+    het = decode.make_heterogeneous_page_gauge_wrapper(
+        None, torch.empty(64 << 20, dtype=torch.uint8, device=device))
+    het.plan(torch.tensor(indptr, dtype=torch.int32), unified, w.tail_last_page_len, 32, 8, 128, 16,
+             exact_tail_pages_hint=16)
+    out_h = torch.empty_like(w.query)
+    het_args = (w.query, (w.k_codes, w.v_codes), w.k_scale, w.v_scale, w.tail_k, w.tail_v,
+                old_kv_len, w.value_center)
+    het.run(*het_args, out=out_h)
+    bounds["heterogeneous"] = lambda: het.run(*het_args, out=out_h)
+    fp16 = decode.BatchDecodeWithPagedKVCacheWrapper(
+        torch.empty(64 << 20, dtype=torch.uint8, device=device), "NHD")
+    fp16.plan(w.fp16_indptr, w.fp16_indices, w.fp16_last_page_len, 32, 8, 128, 16,
+              kv_data_type=torch.float16)
+    out16 = torch.empty_like(w.query)
+    bounds["fp16"] = fp16.bind(w.query, (w.fp16_k, w.fp16_v), out=out16, lse=torch.empty_like(lse))
+    res = {"lengths": w.lengths, "algorithmic_bytes": {"page_gauge": w.algorithmic_bytes(),
+                                                       "fp16": w.fp16_algorithmic_bytes()}}
+    for name, call in bounds.items():
+        for _ in range(3):
+            scrub()
+            call()
+        ms = call_samples(torch, call, samples, scrub)
+        mean_us = 1e3 * statistics.fmean(ms)
+        res[name] = {"call_mean_us": round(mean_us, 2),
+                     "call_p50_us": round(1e3 * statistics.median(ms), 2),
+                     "rtx5090_paper_mean_us": PAPER_B4_20K_RTX5090_US[name],
+                     "rtx5090_over_this": round(PAPER_B4_20K_RTX5090_US[name] / mean_us, 2)}
+    torch.cuda.synchronize()
+    res["heterogeneous_vs_segmented_max_abs"] = float((out_h.float() - out.float()).abs().max())
+    res["fp16_over_segmented"] = round(res["fp16"]["call_mean_us"] / res["segmented"]["call_mean_us"],
+                                       3)
+    return res
+
+
 def update_config4(torch, device, replays: int):
     """Config 4 cache update: B=8, 16 decode steps (start lengths
     4096, 4099, ..., 16398: every row closes one page, four of them mid-window),
@@ -522,6 +590,7 @@ def main() -> int:
             torch.cuda.empty_cache()
         other["config3_b8_ragged"] = ragged
         other["config4_update"] = update_config4(torch, device, 50)
+        other["paper_b4_20k"] = paper_b4_20k(torch, decode, workloads, device, scrub_clean, 60)
     if not args.no_decoder:
         other = other or {}
         other["config5_decoder"] = decoder_config5(torch, device, args.decoder_repeats)

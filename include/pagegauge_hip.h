@@ -260,17 +260,23 @@ int32_t pg_select_split_pages(int64_t total_pages, int32_t batch_size, int32_t n
  * the tail likewise with tail_split_pages, default ceil(split_pages/2) for
  * INT8 (an FP16 page streams twice the bytes);
  * split_pages <= 0 balances the batch over num_cus workgroups (every item at
- * most 64 pages, FP16 pages weighted twice INT8 pages).  Writes the work list
- * into the device workspace (synchronous copy on ``stream``).  Replaces
- * BatchDecodeWithPagedKVCacheWrapper.plan as called by
+ * most 64 pages, FP16 pages weighted twice INT8 pages).
+ * exact_tail_pages_hint (heterogeneous plans only, else 0): the number of
+ * trailing pages of each request's unified table expected to be FP16 exact
+ * pages at run time; they are planned like a tail segment (own items,
+ * weighted as FP16 pages).  It only balances the work: the kernel reads
+ * old_kv_len at run time, so any boundary is handled correctly.  (A builder
+ * addition: the reference's heterogeneous plan has no such argument.)
+ * Writes the work list into the device workspace (synchronous copy on
+ * ``stream``).  Replaces BatchDecodeWithPagedKVCacheWrapper.plan as called by
  * scripts/benchmark_flashinfer_page_affine_int8.py:363-389. */
 int32_t pg_decode_plan(const int32_t* host_indptr, const int32_t* host_last_page_len,
                        int32_t batch_size, int32_t primary_kind,
                        const int32_t* host_tail_indptr, const int32_t* host_tail_last_len,
                        int32_t num_qo_heads, int32_t num_kv_heads, int32_t head_dim,
                        int32_t page_size, int32_t split_pages, int32_t tail_split_pages,
-                       int32_t num_cus, void* workspace, int64_t workspace_bytes,
-                       pg_decode_plan_t* plan, void* stream);
+                       int32_t exact_tail_pages_hint, int32_t num_cus, void* workspace,
+                       int64_t workspace_bytes, pg_decode_plan_t* plan, void* stream);
 
 /* The host half of pg_decode_plan (same arguments, same validation and
  * errors) without a device: fills *plan and, if items_out != NULL, the work
@@ -286,8 +292,9 @@ int32_t pg_decode_plan_host(const int32_t* host_indptr, const int32_t* host_last
                             const int32_t* host_tail_indptr, const int32_t* host_tail_last_len,
                             int32_t num_qo_heads, int32_t num_kv_heads, int32_t head_dim,
                             int32_t page_size, int32_t split_pages, int32_t tail_split_pages,
-                            int32_t num_cus, pg_decode_plan_t* plan, int32_t* items_out,
-                            int64_t items_capacity, int32_t* item_ptr_out);
+                            int32_t exact_tail_pages_hint, int32_t num_cus,
+                            pg_decode_plan_t* plan, int32_t* items_out, int64_t items_capacity,
+                            int32_t* item_ptr_out);
 
 /* Run a planned decode.  Segment 0: pages ``indices`` (indptr/last_page_len
  * as planned; last_page_len is re-read on the device every call, so a

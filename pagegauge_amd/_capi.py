@@ -12,7 +12,7 @@ import threading
 from pathlib import Path
 
 LIBRARY_PATH = Path(__file__).resolve().parent / "lib" / "libpagegauge_hip.so"
-ABI_VERSION = 3
+ABI_VERSION = 4
 
 PG_OK = 0
 PG_KV_INT8 = 0
@@ -82,9 +82,9 @@ PROTOTYPES = {
     "pg_decode_workspace_bytes": (_i64, [_i32, _i32, _i64, _i64]),
     "pg_select_split_pages": (_i32, [_i64, _i32, _i32, _i32, _i32]),
     "pg_decode_plan": (_i32, [_p, _p, _i32, _i32, _p, _p, _i32, _i32, _i32, _i32, _i32, _i32,
-                              _i32, _p, _i64, ctypes.POINTER(DecodePlan), _p]),
+                              _i32, _i32, _p, _i64, ctypes.POINTER(DecodePlan), _p]),
     "pg_decode_plan_host": (_i32, [_p, _p, _i32, _i32, _p, _p, _i32, _i32, _i32, _i32, _i32,
-                                   _i32, _i32, ctypes.POINTER(DecodePlan), _p, _i64, _p]),
+                                   _i32, _i32, _i32, ctypes.POINTER(DecodePlan), _p, _i64, _p]),
     "pg_decode_run": (_i32, [ctypes.POINTER(DecodePlan), _p, _i64, _p, _p, _p, _p, _p, _p, _p, _p,
                              _p, _p, _p, _i64, _p, _p, _f32, _p, _p]),
     "pg_decode_run_timed": (_i32, [ctypes.POINTER(DecodePlan), _p, _i64, _p, _p, _p, _p, _p, _p,

@@ -1052,8 +1052,9 @@ int32_t build_plan(const int32_t* host_indptr, const int32_t* host_last_page_len
                    int32_t batch_size, int32_t primary_kind, const int32_t* host_tail_indptr,
                    const int32_t* host_tail_last_len, int32_t num_qo_heads, int32_t num_kv_heads,
                    int32_t head_dim, int32_t page_size, int32_t split_pages,
-                   int32_t tail_split_pages, int32_t num_cus, std::vector<WorkItem>& items,
-                   std::vector<int32_t>& item_ptr, pg_decode_plan_t& p) {
+                   int32_t tail_split_pages, int32_t exact_tail_pages_hint, int32_t num_cus,
+                   std::vector<WorkItem>& items, std::vector<int32_t>& item_ptr,
+                   pg_decode_plan_t& p) {
   if (!host_indptr || !host_last_page_len)
     return fail(PG_ERROR_INVALID_ARGUMENT, "null plan argument");
   if (batch_size <= 0) return fail(PG_ERROR_INVALID_ARGUMENT, "batch size must be positive");
@@ -1069,6 +1070,10 @@ int32_t build_plan(const int32_t* host_indptr, const int32_t* host_last_page_len
     return fail(PG_ERROR_INVALID_ARGUMENT, "a heterogeneous plan has one unified page table");
   if ((host_tail_indptr == nullptr) != (host_tail_last_len == nullptr))
     return fail(PG_ERROR_INVALID_ARGUMENT, "tail indptr and last_page_len go together");
+  if (exact_tail_pages_hint < 0)
+    return fail(PG_ERROR_INVALID_ARGUMENT, "exact_tail_pages_hint must be non-negative");
+  if (exact_tail_pages_hint > 0 && primary_kind != PG_KV_HETEROGENEOUS)
+    return fail(PG_ERROR_INVALID_ARGUMENT, "exact_tail_pages_hint applies to heterogeneous plans");
 
   int64_t primary_pages = 0, tail_pages = 0;
   for (int b = 0; b < batch_size; ++b) {
@@ -1086,17 +1091,30 @@ int32_t build_plan(const int32_t* host_indptr, const int32_t* host_last_page_len
     }
   }
   // Segments of the batch; FP16 pages stream twice the bytes of INT8 pages.
+  // ``first`` / ``last``: the request's first and last page in the segment's
+  // page table (a heterogeneous table split by the hint keeps both).
   struct Segment {
     int request, kind, seg, begin, end;
     double weight;
+    int first, last;
   };
   std::vector<Segment> segments;
   for (int b = 0; b < batch_size; ++b) {
     if (host_tail_indptr && host_tail_indptr[b + 1] > host_tail_indptr[b])
       segments.push_back({b, PG_KV_FP16, 1, host_tail_indptr[b], host_tail_indptr[b + 1],
-                          primary_kind == PG_KV_INT8 ? 2.0 : 1.0});
-    if (host_indptr[b + 1] > host_indptr[b])
-      segments.push_back({b, primary_kind, 0, host_indptr[b], host_indptr[b + 1], 1.0});
+                          primary_kind == PG_KV_INT8 ? 2.0 : 1.0, host_tail_indptr[b],
+                          host_tail_indptr[b + 1] - 1});
+    const int begin = host_indptr[b], end = host_indptr[b + 1];
+    if (end <= begin) continue;
+    // heterogeneous table: its last exact_tail_pages_hint pages are expected
+    // to be FP16 exact pages at run time; they are planned as FP16 pages (own
+    // items, first, twice the weight).  Balance only: the kernel reads
+    // old_kv_len at run time, so any boundary is handled correctly.
+    const int exact = std::min(exact_tail_pages_hint, end - begin);
+    if (exact > 0)
+      segments.push_back({b, primary_kind, 0, end - exact, end, 2.0, begin, end - 1});
+    if (end - exact > begin)
+      segments.push_back({b, primary_kind, 0, begin, end - exact, 1.0, begin, end - 1});
   }
   std::vector<int> chunks(segments.size(), 0);
   bool medium = false;
@@ -1169,8 +1187,8 @@ int32_t build_plan(const int32_t* host_indptr, const int32_t* host_last_page_len
       int start = sg.begin;
       for (int k = 0; k < c; ++k) {
         const int size = n / c + (k < n % c ? 1 : 0);
-        items.push_back(WorkItem{b, sg.kind, sg.seg, start, start + size, sg.end - 1,
-                                 static_cast<int32_t>(items.size()) - item_ptr[b], 0, sg.begin,
+        items.push_back(WorkItem{b, sg.kind, sg.seg, start, start + size, sg.last,
+                                 static_cast<int32_t>(items.size()) - item_ptr[b], 0, sg.first,
                                  {0, 0, 0}});
         start += size;
         if (sg.seg == 0) split_pages = std::max(split_pages, size);
@@ -1248,9 +1266,9 @@ extern "C" int32_t pg_decode_plan(const int32_t* host_indptr, const int32_t* hos
                                   const int32_t* host_tail_indptr,
                                   const int32_t* host_tail_last_len, int32_t num_qo_heads,
                                   int32_t num_kv_heads, int32_t head_dim, int32_t page_size,
-                                  int32_t split_pages, int32_t tail_split_pages, int32_t num_cus,
-                                  void* workspace, int64_t workspace_bytes, pg_decode_plan_t* plan,
-                                  void* stream) {
+                                  int32_t split_pages, int32_t tail_split_pages,
+                                  int32_t exact_tail_pages_hint, int32_t num_cus, void* workspace,
+                                  int64_t workspace_bytes, pg_decode_plan_t* plan, void* stream) {
   clear_error();
   if (!plan || !workspace) return fail(PG_ERROR_INVALID_ARGUMENT, "null plan argument");
   std::vector<WorkItem> items;
@@ -1258,8 +1276,8 @@ extern "C" int32_t pg_decode_plan(const int32_t* host_indptr, const int32_t* hos
   pg_decode_plan_t p{};
   const int32_t rc = build_plan(host_indptr, host_last_page_len, batch_size, primary_kind,
                                 host_tail_indptr, host_tail_last_len, num_qo_heads, num_kv_heads,
-                                head_dim, page_size, split_pages, tail_split_pages, num_cus, items,
-                                item_ptr, p);
+                                head_dim, page_size, split_pages, tail_split_pages,
+                                exact_tail_pages_hint, num_cus, items, item_ptr, p);
   if (rc != PG_OK) return rc;
   if (p.workspace_bytes > workspace_bytes)
     return fail(PG_ERROR_WORKSPACE, "decode workspace too small: need " +
@@ -1287,9 +1305,9 @@ extern "C" int32_t pg_decode_plan_host(const int32_t* host_indptr,
                                        const int32_t* host_tail_last_len, int32_t num_qo_heads,
                                        int32_t num_kv_heads, int32_t head_dim, int32_t page_size,
                                        int32_t split_pages, int32_t tail_split_pages,
-                                       int32_t num_cus, pg_decode_plan_t* plan,
-                                       int32_t* items_out, int64_t items_capacity,
-                                       int32_t* item_ptr_out) {
+                                       int32_t exact_tail_pages_hint, int32_t num_cus,
+                                       pg_decode_plan_t* plan, int32_t* items_out,
+                                       int64_t items_capacity, int32_t* item_ptr_out) {
   clear_error();
   if (!plan) return fail(PG_ERROR_INVALID_ARGUMENT, "null plan argument");
   std::vector<WorkItem> items;
@@ -1297,8 +1315,8 @@ extern "C" int32_t pg_decode_plan_host(const int32_t* host_indptr,
   pg_decode_plan_t p{};
   const int32_t rc = build_plan(host_indptr, host_last_page_len, batch_size, primary_kind,
                                 host_tail_indptr, host_tail_last_len, num_qo_heads, num_kv_heads,
-                                head_dim, page_size, split_pages, tail_split_pages, num_cus, items,
-                                item_ptr, p);
+                                head_dim, page_size, split_pages, tail_split_pages,
+                                exact_tail_pages_hint, num_cus, items, item_ptr, p);
   if (rc != PG_OK) return rc;
   *plan = p;
   if (items_out) {

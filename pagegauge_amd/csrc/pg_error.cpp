@@ -16,4 +16,4 @@ void clear_error() { g_last_error.clear(); }
 
 extern "C" const char* pg_last_error(void) { return pg::g_last_error.c_str(); }
 
-extern "C" int32_t pg_abi_version(void) { return 3; }
+extern "C" int32_t pg_abi_version(void) { return 4; }

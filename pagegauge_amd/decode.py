@@ -105,7 +105,7 @@ class _Planned:
 
     def make_plan(self, host_indptr, host_last, primary_kind, host_tail_indptr, host_tail_last,
                   num_qo_heads, num_kv_heads, head_dim, page_size, split_pages, tail_split_pages,
-                  device, num_cus: Optional[int] = None) -> None:
+                  device, num_cus: Optional[int] = None, exact_tail_pages_hint: int = 0) -> None:
         lib = _capi.library()
         batch = host_indptr.numel() - 1
         rc = lib.pg_decode_plan(
@@ -113,8 +113,8 @@ class _Planned:
             None if host_tail_indptr is None else host_tail_indptr.data_ptr(),
             None if host_tail_last is None else host_tail_last.data_ptr(),
             num_qo_heads, num_kv_heads, head_dim, page_size, int(split_pages or 0),
-            int(tail_split_pages or 0), int(num_cus or _num_cus(device)), self.workspace.data_ptr(),
-            self.workspace.numel(), ctypes.byref(self.plan), _stream())
+            int(tail_split_pages or 0), int(exact_tail_pages_hint), int(num_cus or _num_cus(device)),
+            self.workspace.data_ptr(), self.workspace.numel(), ctypes.byref(self.plan), _stream())
         _capi.check(rc, "decode plan")
         self.planned = True
         self.generation += 1
@@ -136,7 +136,7 @@ WORK_ITEM_FIELDS = ("request", "kind", "segment", "page_begin", "page_end", "las
 def plan_work_items(indptr, last_page_len, tail_indptr=None, tail_last_page_len=None,
                     kv_data_type=torch.int8, num_qo_heads: int = HQ, num_kv_heads: int = HKV,
                     head_dim: int = DIM, page_size: int = PAGE, split_pages: int = 0,
-                    tail_split_pages: int = 0, num_cus: int = 256):
+                    tail_split_pages: int = 0, num_cus: int = 256, exact_tail_pages_hint: int = 0):
     """Run the decode scheduler on the host only (no device, no workspace).
 
     Returns ``(plan, items, item_ptr)``: the ``DecodePlan`` that
@@ -157,7 +157,7 @@ def plan_work_items(indptr, last_page_len, tail_indptr=None, tail_last_page_len=
             None if host_tail is None else host_tail.data_ptr(),
             None if host_tail_last is None else host_tail_last.data_ptr(), num_qo_heads,
             num_kv_heads, head_dim, page_size, int(split_pages), int(tail_split_pages),
-            int(num_cus), ctypes.byref(plan))
+            int(exact_tail_pages_hint), int(num_cus), ctypes.byref(plan))
     _capi.check(lib.pg_decode_plan_host(*args, None, 0, None), "decode plan")
     items = torch.empty(max(1, plan.num_items), len(WORK_ITEM_FIELDS), dtype=torch.int32)
     item_ptr = torch.empty(batch + 1, dtype=torch.int32)
@@ -543,7 +543,12 @@ class HeterogeneousDecodeWrapper:
              pos_encoding_mode: str = "NONE", q_data_type=torch.float16,
              kv_data_type=torch.int8, o_data_type=torch.float16, sm_scale=None,
              fixed_split_size: Optional[int] = None, num_cus: Optional[int] = None,
-             **_unused) -> None:
+             exact_tail_pages_hint: int = 0, **_unused) -> None:
+        """``exact_tail_pages_hint`` (a builder addition): how many trailing
+        pages of each request's table are expected to be FP16 exact pages at
+        run time; the planner gives them their own work items, weighted as
+        FP16 pages.  It only balances the work; ``old_kv_len`` still decides
+        the boundary at run time."""
         if pos_encoding_mode != "NONE":
             raise ValueError("only pos_encoding_mode='NONE' is supported")
         if kv_data_type != torch.int8 or q_data_type != torch.float16 or o_data_type != torch.float16:
@@ -553,7 +558,8 @@ class HeterogeneousDecodeWrapper:
         host_indptr = _host_i32(indptr)
         self._state.make_plan(host_indptr, _host_i32(last_page_len), _capi.PG_KV_HETEROGENEOUS,
                               None, None, num_qo_heads, num_kv_heads, head_dim, page_size,
-                              fixed_split_size or 0, 0, indices.device, num_cus)
+                              fixed_split_size or 0, 0, indices.device, num_cus,
+                              exact_tail_pages_hint)
         self._indices = indices
         self._last_page_len = last_page_len
         self._batch = host_indptr.numel() - 1

@@ -631,7 +631,8 @@ class PageGaugeDecoder:
                                self.split_pages, page_table_epoch=self.heterogeneous_page_table_updates):
                 self.decode.plan(self.table.host_indptr, self.table.active_indices(),
                                  self.table.last_len, self.config.q_heads, self.config.kv_heads,
-                                 DIM, PAGE, fixed_split_size=self.split_pages or None)
+                                 DIM, PAGE, fixed_split_size=self.split_pages or None,
+                                 exact_tail_pages_hint=self.exact_pages)
                 self.kernel_replans += 1
             self.plan_signature_value = ("heterogeneous", self.table.signature)
             return

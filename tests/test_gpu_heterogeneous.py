@@ -85,12 +85,13 @@ def _device(f, cuda):
     return {k: torch.from_numpy(np.ascontiguousarray(v)).to(cuda) for k, v in f.items()}
 
 
-def _run(d, split, cuda):
+def _run(d, split, cuda, hint=0):
     from pagegauge_amd import decode
 
     ws = torch.empty(8 << 20, dtype=torch.uint8, device=cuda)
     wrapper = decode.make_heterogeneous_page_gauge_wrapper(None, ws)
-    wrapper.plan(d["indptr"], d["indices"], d["last"], 32, 8, 128, 16, fixed_split_size=split or None)
+    wrapper.plan(d["indptr"], d["indices"], d["last"], 32, 8, 128, 16, fixed_split_size=split or None,
+                 exact_tail_pages_hint=hint)
     decode.validate_heterogeneous_run_inputs(d["query"], d["k_codes"], d["v_codes"], d["k_scale"],
                                              d["v_scale"], d["exact_k"], d["exact_v"], d["old_len"],
                                              d["center"])
@@ -108,6 +109,21 @@ def test_heterogeneous_matches_oracle(cuda, name, old_tokens, total_tokens, ring
     f = _fixture(old_tokens, total_tokens, ring_pages, batch=3, seed=sum(map(ord, name)) + split)
     want16, want_lse, _ = _oracle(f)
     _, out, lse = _run(_device(f, cuda), split, cuda)
+    assert torch.isfinite(out).all() and torch.isfinite(lse).all()
+    assert max_abs(out, want16) <= 2e-3, name
+    assert max_abs(lse, want_lse) <= 2e-3, name
+
+
+@pytest.mark.parametrize("hint", [1, 4, 40])
+@pytest.mark.parametrize("name,old_tokens,total_tokens,ring_pages", CASES)
+def test_exact_tail_hint_changes_balance_not_results(cuda, name, old_tokens, total_tokens,
+                                                      ring_pages, hint):
+    """The planning hint may match the real INT8/FP16 boundary or not (1 and
+    40 trailing pages against rings of 1-4 pages); results stay the oracle's."""
+    print(f"heterogeneous hint {name} hint={hint}", flush=True)
+    f = _fixture(old_tokens, total_tokens, ring_pages, batch=3, seed=sum(map(ord, name)) + hint)
+    want16, want_lse, _ = _oracle(f)
+    _, out, lse = _run(_device(f, cuda), 0, cuda, hint=hint)
     assert torch.isfinite(out).all() and torch.isfinite(lse).all()
     assert max_abs(out, want16) <= 2e-3, name
     assert max_abs(lse, want_lse) <= 2e-3, name

@@ -159,3 +159,34 @@ def test_batches_keep_the_item_table():
     plan, _, _ = plan_work_items([0, 100, 240], [16, 16], [0, 16, 32], [16, 16])
     assert plan.closed_form == 0
     assert (plan.cf_tail_items, plan.cf_primary_pages) == (0, 0)
+
+
+@pytest.mark.parametrize("pages,hint", [([1280] * 4, 16), ([37, 5, 900], 16), ([12], 16), ([64], 3)])
+def test_heterogeneous_hint_gives_the_ring_its_own_items(pages, hint):
+    """exact_tail_pages_hint: the last ``hint`` pages of each unified table
+    form items of their own, weighted as FP16 pages; every item keeps the
+    request's first and last page, and the table is still covered once."""
+    ptr = _indptr(pages)
+    plan, items, item_ptr = plan_work_items(ptr, [16] * len(pages), kv_data_type="heterogeneous",
+                                            exact_tail_pages_hint=hint)
+    _check_cover(items, item_ptr.tolist(), pages, [0] * len(pages))
+    it = items.numpy()
+    for b, n in enumerate(pages):
+        mine = it[it[:, 0] == b]
+        assert (mine[:, 8] == ptr[b]).all()                       # request_page_begin
+        assert (mine[:, 5] == ptr[b + 1] - 1).all()               # the request's last page
+        split = ptr[b + 1] - min(hint, n)
+        assert not ((mine[:, 3] < split) & (mine[:, 4] > split)).any()   # no item straddles it
+    if pages == [1280] * 4:
+        size = it[:, 4] - it[:, 3]
+        ring = it[:, 3] >= np.repeat(np.array(ptr[1:]) - hint, [int((it[:, 0] == b).sum())
+                                                                 for b in range(4)])
+        # FP16 items hold about half the pages of INT8 items (equal weighted load)
+        assert size[ring].max() * 2 <= size[~ring].max() + 2
+
+
+def test_exact_tail_hint_is_checked():
+    with pytest.raises(RuntimeError, match="applies to heterogeneous plans"):
+        plan_work_items([0, 100], [16], exact_tail_pages_hint=16)
+    with pytest.raises(RuntimeError, match="must be non-negative"):
+        plan_work_items([0, 100], [16], kv_data_type="heterogeneous", exact_tail_pages_hint=-1)
