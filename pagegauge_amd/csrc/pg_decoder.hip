@@ -19,8 +19,10 @@
 //     FP16 tail pass (pg_decode_run_finalize).
 //
 // The work is HBM-bound weight streaming (M = batch <= 4): every weight byte
-// is read once.  A workgroup (4 waves) owns a group of rows; the 512-element
-// chunks of a row are split over its waves (kC consecutive chunks each), a
+// is read once.  A workgroup (4 waves; 7 for the 14336-wide down
+// projection, whose 4-chunk waves fit occupancy 5) owns a group of rows; the
+// 512-element chunks of a row are split over its waves (kC consecutive
+// chunks each), a
 // lane reads 16 bytes of every chunk (a wave covers 1 KiB per load
 // instruction, fully coalesced), and every weight load of the group is issued
 // before anything else, the input included.  Each wave then loads only its
@@ -54,7 +56,11 @@ constexpr size_t kMaxStagedBytes = 64 * 1024;   // generic kernel: input staged 
 #define PG_GEMV_ROWS_4096_LARGE 4
 #endif
 #ifndef PG_GEMV_ROWS_14336
-#define PG_GEMV_ROWS_14336 2
+#define PG_GEMV_ROWS_14336 4
+#endif
+// Waves per workgroup for k = 14336 (28 chunks of 512 split evenly).
+#ifndef PG_GEMV_WAVES_14336
+#define PG_GEMV_WAVES_14336 7
 #endif
 
 // Cache update of a decode step, applied to the QKV projection's output.
@@ -283,15 +289,15 @@ __device__ __forceinline__ void load_rows(const GemvArgs& a, int row0, int wave,
   }
 }
 
-// Blocked kernel: k = 4 * kC * 512.  kR output rows per workgroup (2*kR
-// weight rows with SwiGLU); grid-stride over row groups when the grid is
-// capped.  kRope: the append epilogue (kR = 2, rows d and d + 64 of a head).
-template <int kBatch, int kR, int kC, bool kSwiglu, bool kRope = false>
-__global__ __launch_bounds__(kGemvThreads) void decoder_gemv_kernel(GemvArgs a) {
+// Blocked kernel: k = kWaves * kC * 512.  kR output rows per workgroup
+// (2*kR weight rows with SwiGLU); grid-stride over row groups when the grid
+// is capped.  kRope: the append epilogue (kR = 2, rows d and d + 64 of a head).
+template <int kBatch, int kR, int kC, bool kSwiglu, bool kRope = false, int kWaves = kGemvWaves>
+__global__ __launch_bounds__(kWave * kWaves) void decoder_gemv_kernel(GemvArgs a) {
   static_assert(!kRope || (kR == 2 && !kSwiglu), "the append epilogue pairs two rows");
   constexpr int kLoad = kSwiglu ? 2 * kR : kR;
-  __shared__ float partial[kGemvWaves][kBatch][kLoad];
-  __shared__ float squares[kGemvWaves][kBatch];
+  __shared__ float partial[kWaves][kBatch][kLoad];
+  __shared__ float squares[kWaves][kBatch];
   const int wave = threadIdx.x / kWave;
   const int lane = threadIdx.x % kWave;
   v4u_t wr[kLoad][kC];
@@ -326,7 +332,7 @@ __global__ __launch_bounds__(kGemvThreads) void decoder_gemv_kernel(GemvArgs a) 
     for (int b = 0; b < kBatch; ++b) {
       float total = 0.0f;
 #pragma unroll
-      for (int w = 0; w < kGemvWaves; ++w) total += squares[w][b];
+      for (int w = 0; w < kWaves; ++w) total += squares[w][b];
       const float inv = rsqrtf(total / static_cast<float>(a.k) + a.eps);
 #pragma unroll
       for (int c = 0; c < kC; ++c) {
@@ -367,7 +373,7 @@ __global__ __launch_bounds__(kGemvThreads) void decoder_gemv_kernel(GemvArgs a) 
       const int b = threadIdx.x;
       float y0 = 0.0f, y1 = 0.0f;
 #pragma unroll
-      for (int w = 0; w < kGemvWaves; ++w) {
+      for (int w = 0; w < kWaves; ++w) {
         y0 += partial[w][b][0];
         y1 += partial[w][b][1];
       }
@@ -379,7 +385,7 @@ __global__ __launch_bounds__(kGemvThreads) void decoder_gemv_kernel(GemvArgs a) 
       if (row < a.out_rows) {
         float y0 = 0.0f, y1 = 0.0f;
 #pragma unroll
-        for (int w = 0; w < kGemvWaves; ++w) {
+        for (int w = 0; w < kWaves; ++w) {
           y0 += partial[w][b][r];
           if (kSwiglu) y1 += partial[w][b][kR + r];
         }
@@ -476,11 +482,11 @@ __global__ __launch_bounds__(kGemvThreads) void decoder_gemv_generic_kernel(Gemv
 template <int kBatch>
 int32_t launch_gemv(GemvArgs a, hipStream_t s) {
   const int chunks = a.k / kChunk;
-  auto blocked = [&](auto kernel, int rows) {
+  auto blocked = [&](auto kernel, int rows, int waves = kGemvWaves) {
     int64_t blocks = (static_cast<int64_t>(a.out_rows) + rows - 1) / rows;
     a.iterations = static_cast<int>((blocks + kMaxBlocks - 1) / kMaxBlocks);
     blocks = (blocks + a.iterations - 1) / a.iterations;
-    hipLaunchKernelGGL(kernel, dim3(static_cast<unsigned>(blocks)), dim3(kGemvThreads), 0, s, a);
+    hipLaunchKernelGGL(kernel, dim3(static_cast<unsigned>(blocks)), dim3(kWave * waves), 0, s, a);
   };
   if (chunks == 8 && !a.swiglu) {                 // k = 4096
     if (a.out_rows > 8192)
@@ -490,7 +496,11 @@ int32_t launch_gemv(GemvArgs a, hipStream_t s) {
   } else if (chunks == 8) {
     blocked(decoder_gemv_kernel<kBatch, PG_GEMV_ROWS_4096, 2, true>, PG_GEMV_ROWS_4096);
   } else if (chunks == 28 && !a.swiglu) {         // k = 14336
-    blocked(decoder_gemv_kernel<kBatch, PG_GEMV_ROWS_14336, 7, false>, PG_GEMV_ROWS_14336);
+    static_assert(28 % PG_GEMV_WAVES_14336 == 0, "k = 14336 splits into whole chunks per wave");
+    constexpr int kWaves14336 = PG_GEMV_WAVES_14336;
+    blocked(decoder_gemv_kernel<kBatch, PG_GEMV_ROWS_14336, 28 / kWaves14336, false, false,
+                                kWaves14336>,
+            PG_GEMV_ROWS_14336, kWaves14336);
   } else {
     const size_t lds = static_cast<size_t>(kBatch) * a.k * sizeof(uint16_t);
     if (lds > kMaxStagedBytes)
