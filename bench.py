@@ -162,6 +162,38 @@ def measure(torch, bound, args, scrub_clean, scrub_rmw):
     return result
 
 
+def controlled_pair(torch, operations: dict, warmup: int, repeats: int, scrub):
+    """The reference's paired protocol (controlled_event_times,
+    scripts/benchmark_flashinfer_page_affine_int8.py:295-349) for two
+    methods: in each repeat both run, in A/B then B/A order alternately;
+    every cache-neutral sample follows a scrub and every cache-hot sample
+    an untimed call of the same method; events bracket the call only.
+    Returns per mode the p50/mean of each method and the p50 ratio B/A."""
+    names = list(operations)
+    out = {}
+    for mode in ("cache_neutral", "cache_hot"):
+        events = {name: [] for name in names}
+        for repeat in range(warmup + repeats):
+            for name in (names if repeat % 2 == 0 else names[::-1]):
+                if mode == "cache_neutral":
+                    scrub()
+                else:
+                    operations[name]()
+                start = torch.cuda.Event(enable_timing=True)
+                end = torch.cuda.Event(enable_timing=True)
+                start.record()
+                operations[name]()
+                end.record()
+                if repeat >= warmup:
+                    events[name].append((start, end))
+        torch.cuda.synchronize()
+        row = {name: summarize([a.elapsed_time(b) for a, b in pairs])
+               for name, pairs in events.items()}
+        row["ratio_p50"] = round(row[names[1]]["p50_us"] / row[names[0]]["p50_us"], 4)
+        out[mode] = row
+    return out
+
+
 def pmc_driver(torch, bound, calls, scrub_clean, device):
     """Workload for one ``rocprofv3 --pmc`` pass (no timing): ``calls`` cold
     decode calls, then ``calls`` plain copies of 64 MiB (64 MiB read + 64 MiB
@@ -565,6 +597,10 @@ def main() -> int:
         fp16["algorithmic_bytes"] = fp16_bytes
         fp16["split_pages"] = wrap16.split_pages
         fp16["achieved_gbps_cold_kernel"] = fp16_bytes / (fp16["cold_clean_1gib"]["kernel"]["mean_us"] * 1e-6) / 1e9
+        # the reference's A/B, B/A paired protocol on the same two calls
+        fp16["paired_with_int8"] = controlled_pair(
+            torch, {"page_gauge_int8": bound, "fp16_same_way": bound16}, 3,
+            max(20, args.steps // 2), scrub_rmw)
 
     sweep = {}
     for item in [s for s in args.sweep.split(",") if s.strip()]:
