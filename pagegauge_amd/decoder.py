@@ -874,11 +874,13 @@ class PageGaugeDecoder:
 def build_decoders(weights: DecoderWeights, prompt: torch.Tensor, decode_steps: int,
                    exact_tail: int = 256, backends=("page_gauge", "fp16"), split_pages: int = 0,
                    exact_sink_pages: int = 0):
-    """Prefill ``prompt`` [T] (T a multiple of 16) once, populate one cache per
-    backend from the same rotated K/V, and return
-    ``(first_token [1], prefill_logits [1,V], {backend: decoder})``."""
+    """Prefill ``prompt`` [T] or [B, T] (T a multiple of 16; every request the
+    same length, as the decoder steps requests in lockstep) once per request,
+    populate one cache per backend from the same rotated K/V, and return
+    ``(first_tokens [B], prefill_logits [B,V], {backend: decoder})``."""
     cfg = weights.config
-    count = int(prompt.numel())
+    prompts = prompt.reshape(1, -1) if prompt.dim() == 1 else prompt
+    batch, count = int(prompts.shape[0]), int(prompts.shape[1])
     if count % PAGE or count <= exact_tail + PAGE * exact_sink_pages:
         raise SystemExit("context and exact tail must be page aligned; context must be larger")
     max_context = count + decode_steps + 1
@@ -888,18 +890,22 @@ def build_decoders(weights: DecoderWeights, prompt: torch.Tensor, decode_steps: 
     cos, sin = cos.to(device), sin.to(device)
     caches = {}
     if "page_gauge" in backends:
-        caches["page_gauge"] = GaugeCache(cfg, 1, pages, exact_tail // PAGE, exact_sink_pages,
+        caches["page_gauge"] = GaugeCache(cfg, batch, pages, exact_tail // PAGE, exact_sink_pages,
                                           device)
     if "fp16" in backends:
-        caches["fp16"] = Fp16Cache(cfg, 1, pages, device)
+        caches["fp16"] = Fp16Cache(cfg, batch, pages, device)
 
-    def on_layer(layer, key, value):
-        for cache in caches.values():
-            cache.populate(layer, 0, key, value)
+    logits = []
+    for request in range(batch):
+        def on_layer(layer, key, value, request=request):
+            for cache in caches.values():
+                cache.populate(layer, request, key, value)
 
-    logits = prefill(weights, prompt.to(device), cos, sin, on_layer)
+        logits.append(prefill(weights, prompts[request].to(device), cos, sin, on_layer))
+    logits = torch.cat(logits)
     first = logits.argmax(dim=-1)
     decoders = {name: PageGaugeDecoder(weights, cache, name, max_context, cos, sin, exact_tail,
-                                       split_pages, 1, exact_sink_pages if name == "page_gauge" else 0)
+                                       split_pages, batch,
+                                       exact_sink_pages if name == "page_gauge" else 0)
                 for name, cache in caches.items()}
     return first, logits, decoders

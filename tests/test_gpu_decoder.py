@@ -238,3 +238,25 @@ def test_fused_cache_update_is_bitwise_the_separate_update(setup, backend, tail,
     if backend == "page_gauge":
         # the page completed at position 527 (logical page 32) was finalized
         assert fused.cache.key_scales[:, 32].abs().min() > 0
+
+
+def test_batched_decoder_steps_requests_in_lockstep(setup):
+    """build_decoders over a [2, T] prompt (one prefill per request, each into
+    its own cache slot): two copies of the same prompt give bitwise the same
+    logits for both requests at every step, and they match the one-request
+    decoder (the split plans differ, so within the attention tolerance)."""
+    dec, weights, first, decoders, tokens = setup
+    cfg = weights.config
+    gen = torch.Generator().manual_seed(20260850)
+    prompt = torch.randint(0, cfg.vocab, (PROMPT,), generator=gen)
+    print("batched decoder B=2", flush=True)
+    first2, logits2, built = dec.build_decoders(weights, torch.stack((prompt, prompt)), STEPS + 1,
+                                                backends=("page_gauge",))
+    batched = built["page_gauge"]
+    single = _fresh(dec, decoders["page_gauge"])
+    assert batched.batch_size == 2 and torch.equal(first2, first.repeat(2))
+    for i in range(STEPS):
+        pair = batched.step(tokens[i].repeat(2), PROMPT + i).clone()
+        one = single.step(tokens[i:i + 1], PROMPT + i).clone()
+        assert torch.equal(pair[0], pair[1]), i
+        assert float((pair[:1] - one).abs().max()) <= 1.6e-2, i
