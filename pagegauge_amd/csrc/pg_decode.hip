@@ -65,6 +65,13 @@ constexpr int kMinChunkPages = 4;       // balanced plans keep at least one PV g
 #define PG_LARGE_BATCH_MIN_CHUNK 16.0
 #endif
 constexpr double kLargeBatchMinChunk = PG_LARGE_BATCH_MIN_CHUNK;  // weighted pages
+// Upper end of the medium regime (weighted pages per CU).  Up to 30, 7/16 of
+// the CUs in items of at most 64 pages (at most 120 items, 240 half-height
+// workgroups) still cover the batch in one wave of workgroups.
+#ifndef PG_MEDIUM_MAX_PAGES_PER_CU
+#define PG_MEDIUM_MAX_PAGES_PER_CU 30.0
+#endif
+constexpr double kMediumMaxPagesPerCu = PG_MEDIUM_MAX_PAGES_PER_CU;
 constexpr float kNegInf = -__builtin_huge_valf();
 
 struct WorkItem {
@@ -1148,19 +1155,20 @@ int32_t build_plan(const int32_t* host_indptr, const int32_t* host_last_page_len
     };
     double lo = 1e-3, hi = 1.0;
     for (const Segment& sg : segments) hi += (sg.end - sg.begin) * sg.weight;
-    // Measured on MI355X (B=1 sweeps from 4K to 49K tokens):
-    // * large (>= 16 pages per CU): 16-page chunks beat finer ones, because
+    // Measured on MI355X (B=1 sweeps from 4K to 160K tokens, B=4 and B=8):
+    // * large (>= 30 pages per CU): 16-page chunks beat finer ones, because
     //   each work item pays a fixed start-up (page ids, then the first
     //   group), on up to one 8-wave workgroup per CU;
-    // * medium (3..16 pages per CU): about 7/16 of the CUs in items, each
+    // * medium (3..30 pages per CU): about 7/16 of the CUs in items, each
     //   split over two half-height workgroups (one wave per SIMD), so every
-    //   wave pipelines 2..7 groups (16K: 12.6 against 13.9 us; 49K: the same
-    //   partial kernel time as 193 items, and a cheaper combine);
+    //   wave pipelines 2..16 groups (16K: 12.6 against 13.9 us; 64K: 29.2
+    //   against 31.3 us; 112K: 45.1 against 47.8 us); past 30 the 64-page
+    //   item cap needs more than 128 items, a second wave of workgroups;
     // * small: chunks down to one PV group for parallelism.
     const double per_cu = hi / static_cast<double>(target);
-    medium = per_cu >= 3.0 && per_cu < 16.0;
+    medium = per_cu >= 3.0 && per_cu < kMediumMaxPagesPerCu;
     const int64_t item_target = medium ? std::max<int64_t>(1, target * 7 / 16) : target;
-    lo = per_cu >= 16.0 ? kLargeBatchMinChunk : 1e-3;
+    lo = per_cu >= kMediumMaxPagesPerCu ? kLargeBatchMinChunk : 1e-3;
     if (count_for(hi, nullptr) <= item_target) {
       for (int iter = 0; iter < 64; ++iter) {
         const double mid = 0.5 * (lo + hi);

@@ -55,11 +55,13 @@ def test_balanced_plan_covers_every_page_once(old, tail):
 
 
 @pytest.mark.parametrize("tokens,items,waves", [(4096, 64, 2), (8192, 128, 4), (16400, 112, 4),
-                                                (49152, 112, 4)])
+                                                (49152, 112, 4), (65536, 112, 4), (114688, 113, 4),
+                                                (131072, 256, 8)])
 def test_one_request_plan_regimes(tokens, items, waves):
-    """Small problems: chunks down to one PV group; medium (3..16 weighted
-    pages per CU, B1/49K included): 7/16 of the CUs in items, each over two
-    half-height workgroups."""
+    """Small problems: chunks down to one PV group; medium (3..30 weighted
+    pages per CU, B1/49K included): 7/16 of the CUs in items (more only where
+    the 64-page item cap needs them), each over two half-height workgroups;
+    large (128K tokens: 32 pages per CU): one 8-wave workgroup per item."""
     old = tokens // 16 - 16
     plan, got, _ = plan_work_items([0, old], [16], [0, 16], [16])
     assert (plan.num_items, plan.waves_per_block) == (items, waves)
