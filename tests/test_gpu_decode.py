@@ -67,6 +67,23 @@ def test_b8_ragged_config3(cuda, workspace, seed):
     assert dec.num_work_items >= 8
 
 
+@pytest.mark.parametrize("lengths", [[28672] * 4, [65536]])
+def test_medium_plans_with_long_items(cuda, workspace, lengths):
+    """Medium-regime plans up to 30 weighted pages per CU: 112-120 items of
+    up to 64 pages (16 groups per wave, the PV accumulators' exactness
+    bound), each over two half-height workgroups."""
+    from pagegauge_amd import workloads
+
+    w = workloads.build_decode_workload(lengths, seed=20260841, device=cuda)
+    out, lse, dec = _segmented(w, workspace)
+    plan = dec._state.plan
+    print("medium", lengths[0], len(lengths), plan.num_items, plan.waves_per_block, flush=True)
+    assert plan.waves_per_block == 4 and 112 <= plan.num_items <= 120
+    ref_out, ref_lse, _ = oracle_decode(w)
+    assert max_abs(out, ref_out) <= OUT_TOL
+    assert max_abs(lse, ref_lse) <= LSE_TOL
+
+
 def test_b1_49k_config2_full_size(cuda, workspace):
     from pagegauge_amd import workloads
 
