@@ -106,3 +106,71 @@ def test_errors_do_not_leak_into_the_next_call():
     assert rc == 1 and text
     rc, text = _call("pg_argmax_f32", FAKE, 1, 0, 10, FAKE, None)
     assert "at least one element" in text and "null" not in text
+
+
+def _host_plan(kind=_capi.PG_KV_INT8, tail=True):
+    """A real plan from the host planner (one request of 100 INT8 pages and a
+    16-page FP16 tail)."""
+    from pagegauge_amd.decode import plan_work_items
+
+    dtype = {_capi.PG_KV_INT8: torch.int8, _capi.PG_KV_HETEROGENEOUS: "heterogeneous"}[kind]
+    plan, _, _ = plan_work_items([0, 100], [16], [0, 16] if tail else None,
+                                 [16] if tail else None, kv_data_type=dtype)
+    return plan
+
+
+def _decode_run(plan, **over):
+    a = dict(plan=ctypes.byref(plan), q=FAKE, qbs=4096, k=FAKE, v=FAKE, ks=FAKE, vs=FAKE, idx=FAKE,
+             last=FAKE, tk=FAKE, tv=FAKE, tidx=FAKE, tlast=FAKE, center=FAKE, cbs=1024, out=FAKE,
+             lse=FAKE, scale=ctypes.c_float(0.088), ws=FAKE, stream=None)
+    a.update(over)
+    return _call("pg_decode_run", *a.values())
+
+
+@pytest.mark.parametrize("over,message", [
+    (dict(q=None), "null run argument"),
+    (dict(ws=None), "null run argument"),
+    (dict(k=None), "primary segment tensors missing"),
+    (dict(ks=None), "INT8 pages need k_scale and v_scale"),
+    (dict(tidx=None), "tail segment tensors missing"),
+    (dict(scale=ctypes.c_float(0.0)), "sm_scale must be positive and finite"),
+    (dict(scale=ctypes.c_float(float("inf"))), "sm_scale must be positive and finite"),
+])
+def test_decode_run_rejects(over, message):
+    rc, text = _decode_run(_host_plan(), **over)
+    assert rc == 1
+    assert message in text
+
+
+def test_decode_run_rejects_a_tampered_plan():
+    plan = _host_plan()
+    plan.waves_per_block = 3
+    rc, text = _decode_run(plan)
+    assert rc == 1 and "invalid waves_per_block" in text
+    plan = _host_plan()
+    assert plan.closed_form == 1
+    plan.cf_tail_items = plan.num_items + 1
+    rc, text = _decode_run(plan)
+    assert rc == 1 and "inconsistent closed-form" in text
+
+
+def test_heterogeneous_plans_and_old_kv_len_go_together():
+    # an INT8 plan given old_kv_len (the heterogeneous entry point)
+    # plan, q, q stride, codes k/v, scales k/v, exact k/v, indices, last_page_len, old_kv_len,
+    # value_center, center stride, out, lse, sm_scale, workspace, stream
+    args = [ctypes.byref(_host_plan()), FAKE, 4096, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE,
+            FAKE, FAKE, 1024, FAKE, FAKE, ctypes.c_float(0.088), FAKE, None]
+    rc, text = _call("pg_decode_run_heterogeneous", *args)
+    assert rc == 1 and "old_kv_len goes with (and only with) a heterogeneous plan" in text
+    # a heterogeneous plan without the exact pages
+    args[0] = ctypes.byref(_host_plan(_capi.PG_KV_HETEROGENEOUS, tail=False))
+    args[7] = None                       # exact_k
+    rc, text = _call("pg_decode_run_heterogeneous", *args)
+    assert rc == 1 and "heterogeneous pages need the exact K/V pages" in text
+
+
+def test_finalize_needs_int8_pages_and_positive_code_pages():
+    args = [ctypes.byref(_host_plan()), FAKE, 4096, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE,
+            FAKE, FAKE, FAKE, 1024, FAKE, FAKE, ctypes.c_float(0.088), FAKE, FAKE, 0, 0, None]
+    rc, text = _call("pg_decode_run_finalize", *args)
+    assert rc == 1 and "positive code pages per request" in text
