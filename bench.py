@@ -551,8 +551,8 @@ def cpu_baseline(w, budget_s: float):
 def main() -> int:
     args = parse_args()
     if args.gpus != 1:
-        print(f"bench.py measures one GPU only (the path is a single-GPU decode; sharding is "
-              f"described in DESIGN.md); --gpus {args.gpus} is not supported", file=sys.stderr)
+        print(f"bench.py measures one GPU only (the path is a single-GPU decode, and this run "
+              f"uses one GPU); --gpus {args.gpus} is not supported", file=sys.stderr)
         return 2
     import numpy as np
     import torch
