@@ -203,10 +203,6 @@ __device__ __forceinline__ void wave_lds_fence() {
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 }
 
-__device__ __forceinline__ int clamp_page_slot(int slot, int begin, int end) {
-  return slot < end ? slot : end - 1;
-}
-
 struct Int8Group {
   v4i k[4][2];      // K codes of page i: bytes 16*kg.. and 64+16*kg.. of token lane%16
   v2u v[16];        // V codes [page i][t]: dims 8*(lane%16).. of token 4*(lane/16)+t
@@ -1082,19 +1078,16 @@ int32_t build_plan(const int32_t* host_indptr, const int32_t* host_last_page_len
   if (exact_tail_pages_hint > 0 && primary_kind != PG_KV_HETEROGENEOUS)
     return fail(PG_ERROR_INVALID_ARGUMENT, "exact_tail_pages_hint applies to heterogeneous plans");
 
-  int64_t primary_pages = 0, tail_pages = 0;
   for (int b = 0; b < batch_size; ++b) {
     const int64_t n = static_cast<int64_t>(host_indptr[b + 1]) - host_indptr[b];
     if (n < 0) return fail(PG_ERROR_INVALID_ARGUMENT, "indptr must be non-decreasing");
     if (n > 0 && (host_last_page_len[b] < 1 || host_last_page_len[b] > kPageSize))
       return fail(PG_ERROR_INVALID_ARGUMENT, "last_page_len must lie in [1, 16]");
-    primary_pages += n;
     if (host_tail_indptr) {
       const int64_t tn = static_cast<int64_t>(host_tail_indptr[b + 1]) - host_tail_indptr[b];
       if (tn < 0) return fail(PG_ERROR_INVALID_ARGUMENT, "tail indptr must be non-decreasing");
       if (tn > 0 && (host_tail_last_len[b] < 1 || host_tail_last_len[b] > kPageSize))
         return fail(PG_ERROR_INVALID_ARGUMENT, "tail last_page_len must lie in [1, 16]");
-      tail_pages += tn;
     }
   }
   // Segments of the batch; FP16 pages stream twice the bytes of INT8 pages.
