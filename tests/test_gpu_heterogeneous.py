@@ -15,7 +15,7 @@ import pytest
 import torch
 
 from oracle import pg_oracle as oracle
-from tests.helpers import cpu, max_abs
+from tests.helpers import max_abs
 
 pytestmark = pytest.mark.gpu
 
