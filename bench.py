@@ -60,6 +60,8 @@ def parse_args() -> argparse.Namespace:
                    help="skip the config-1/3 decode lines and the config-4 update timing")
     p.add_argument("--sweep", default="", help="comma list of split sizes to time (pilot sweep)")
     p.add_argument("--no-decoder", action="store_true", help="skip the config-5 decoder line")
+    p.add_argument("--paper-only", action="store_true",
+                   help="print only the reference paper's B4 x 20K isolated-attention line")
     p.add_argument("--decoder-only", action="store_true",
                    help="run only the config-5 decoder and print its JSON")
     p.add_argument("--decoder-repeats", type=int, default=5)
@@ -566,6 +568,12 @@ def main() -> int:
     torch.cuda.set_device(device)
     if args.decoder_only:
         print(json.dumps(decoder_config5(torch, device, args.decoder_repeats)), flush=True)
+        return 0
+    if args.paper_only:
+        buf = torch.ones((args.big_scrub_mib << 20) // 4, dtype=torch.int32, device=device)
+        sink = torch.empty((), dtype=torch.int32, device=device)
+        print(json.dumps(paper_b4_20k(torch, decode, workloads, device,
+                                      lambda: torch.amax(buf, dim=0, out=sink), 60)), flush=True)
         return 0
     t_setup = time.perf_counter()
     w = workloads.b1_49k(args.seed, device=device, with_fp16_copy=not args.no_fp16)
