@@ -8,9 +8,16 @@ call signatures:
   completed-page INT8 finalize, the fused exact-tail merge;
 * ``decode`` -- paged decode over INT8 page-affine and FP16 pages
   (``BatchDecodeWithPagedKVCacheWrapper``, ``make_page_gauge_wrapper``,
-  ``PageGaugeSegmentedDecode``, ``merge_state_in_place``);
+  ``PageGaugeSegmentedDecode``, the heterogeneous one-table wrapper,
+  ``merge_state_in_place``) and the split scheduler (``plan_work_items``);
+* ``update`` -- the paged append / finalize, bulk quantizers, prefill
+  population and exact centers;
 * ``page_table`` -- the page-table algebra of the decoder harness;
-* ``scheduler`` -- split-KV selection for 256 CUs.
+* ``decoder`` -- the Mistral-shaped decoder over these kernels;
+* ``serving`` / ``serving_bridge`` -- request slots, decode-batch tables and
+  the scheduler bridge;
+* ``workloads`` -- the seeded benchmark configurations.
 """
 
-__all__ = ["runtime", "decode", "page_table", "scheduler", "workloads"]
+__all__ = ["runtime", "decode", "update", "page_table", "decoder", "serving", "serving_bridge",
+           "workloads"]

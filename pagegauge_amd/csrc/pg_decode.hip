@@ -215,11 +215,16 @@ __device__ __forceinline__ uint32_t digit_bytes(int x) {
   return static_cast<uint32_t>(x + 0x808080) ^ 0x808080u;
 }
 
-// Exact-integer recombination of the three digit rows of an accumulator:
-// 65536*acc.x + 256*acc.y + acc.z with |acc.y| < 2^21, |acc.z| < 2^21.
+// Recombination of the three digit rows of an accumulator:
+// 65536*acc.x + 256*acc.y + acc.z for |acc.x|, |acc.y|, |acc.z| < 2^24.
+// Each row converts to float exactly, and the fused multiply-add rounds
+// 256*acc.y + acc.z once, so the low part is the correctly rounded value of
+// the exact integer.  That integer can exceed int32: the PV accumulators of
+// a 64-page item sum up to 16 groups of 64 tokens x 128 x 127 < 2^24 per
+// row, i.e. 256*acc.y up to 2^32.
 __device__ __forceinline__ float from_digits(v4i acc) {
-  const int low = (acc.y << 8) + acc.z;
-  return static_cast<float>(acc.x) * 65536.0f + static_cast<float>(low);
+  const float low = fmaf(static_cast<float>(acc.y), 256.0f, static_cast<float>(acc.z));
+  return static_cast<float>(acc.x) * 65536.0f + low;
 }
 
 // Online-softmax update for chunks whose first step has a visible token (so
@@ -388,8 +393,9 @@ __device__ __forceinline__ void int8_chunk(const DecodeArgs& a, const WorkItem& 
   // PV partial sums stay in the MFMA accumulators (exact int32) while the
   // running max is unchanged; they are folded into st.o when it rises and at
   // the end.  Per digit row and group the sum is below 64 tokens * 128 * 127
-  // < 2^20, so 16 groups (the 64-page chunk bound) stay below 2^24 (exact in
-  // float as well).
+  // < 2^20, so 16 groups (the 64-page chunk bound) stay below 2^24: each row
+  // is exact in float, and from_digits recombines the rows in float (256 x
+  // the middle row alone can pass 2^31).
   v4i pv[8];
 #pragma unroll
   for (int nb = 0; nb < 8; ++nb) pv[nb] = v4i{0, 0, 0, 0};

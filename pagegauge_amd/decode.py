@@ -20,6 +20,7 @@ from __future__ import annotations
 
 import ctypes
 import math
+import os
 from typing import Optional, Sequence
 
 import torch
@@ -51,6 +52,59 @@ def _host_i32(tensor: torch.Tensor | Sequence[int]) -> torch.Tensor:
 
 def _ptr(tensor: Optional[torch.Tensor]):
     return None if tensor is None else tensor.data_ptr()
+
+
+def _host_tables(indptr, last_page_len, indices: Optional[torch.Tensor] = None,
+                 what: str = "") -> tuple[torch.Tensor, torch.Tensor]:
+    """Host int32 copies of a CSR page table's ``indptr`` and
+    ``last_page_len``, checked against each other and against ``indices``
+    (its length only) before the planner reads them: the planner reads
+    ``last_page_len[b]`` for every request and the kernels read
+    ``indices[indptr[0]:indptr[B]]``, so a short tensor would be read past
+    its end."""
+    prefix = f"{what} " if what else ""
+    host_indptr = _host_i32(indptr)
+    host_last = _host_i32(last_page_len)
+    if host_indptr.dim() != 1 or host_indptr.numel() < 2:
+        raise ValueError(f"{prefix}indptr must be a 1-D tensor of batch_size + 1 >= 2 entries")
+    batch = host_indptr.numel() - 1
+    if host_last.dim() != 1 or host_last.numel() != batch:
+        raise ValueError(f"{prefix}last_page_len must have one entry per request "
+                         f"({batch}), got {host_last.numel()}")
+    if int(host_indptr[0]) < 0:
+        raise ValueError(f"{prefix}indptr[0] must be non-negative")
+    if batch > 0 and bool((host_indptr[1:] < host_indptr[:-1]).any()):
+        raise ValueError(f"{prefix}indptr must be non-decreasing")
+    if indices is not None and indices.numel() < int(host_indptr[-1]):
+        raise ValueError(f"{prefix}indices has {indices.numel()} entries but indptr[-1] is "
+                         f"{int(host_indptr[-1])}")
+    return host_indptr, host_last
+
+
+# Opt-in page-id bounds check (debug builds of a caller): with
+# PAGEGAUGE_CHECK_PAGE_IDS=1 in the environment (or ``CHECK_PAGE_IDS = True``
+# set on this module), ``plan()`` copies the planned page ids to the host and
+# every ``run()`` / ``bind()`` verifies that they index the pools it is given.
+# The kernels themselves trust the tables, as the reference's do.
+CHECK_PAGE_IDS = os.environ.get("PAGEGAUGE_CHECK_PAGE_IDS", "0") not in ("", "0")
+
+
+def _page_id_range(indices: torch.Tensor, host_indptr: torch.Tensor):
+    """(min, max) of the planned ids ``indices[indptr[0]:indptr[-1]]``, or
+    None when the check is off or the table is empty."""
+    if not CHECK_PAGE_IDS:
+        return None
+    lo, hi = int(host_indptr[0]), int(host_indptr[-1])
+    if hi <= lo:
+        return None
+    ids = indices[lo:hi].detach().to("cpu")
+    return int(ids.min()), int(ids.max())
+
+
+def _check_page_ids(id_range, pool_pages: int, what: str) -> None:
+    if id_range is not None and (id_range[0] < 0 or id_range[1] >= pool_pages):
+        raise ValueError(f"{what} page ids span [{id_range[0]}, {id_range[1]}] but the pool "
+                         f"holds {pool_pages} pages")
 
 
 def _check_query(q: torch.Tensor, batch: int, num_qo_heads: int) -> None:
@@ -145,10 +199,14 @@ def plan_work_items(indptr, last_page_len, tail_indptr=None, tail_last_page_len=
     item offsets.  Same validation and error messages as ``plan``.
     """
     lib = _capi.library()
-    host_indptr = _host_i32(indptr)
-    host_last = _host_i32(last_page_len)
-    host_tail = None if tail_indptr is None else _host_i32(tail_indptr)
-    host_tail_last = None if tail_last_page_len is None else _host_i32(tail_last_page_len)
+    host_indptr, host_last = _host_tables(indptr, last_page_len)
+    host_tail = host_tail_last = None
+    if (tail_indptr is None) != (tail_last_page_len is None):
+        raise ValueError("tail indptr and last_page_len go together")
+    if tail_indptr is not None:
+        host_tail, host_tail_last = _host_tables(tail_indptr, tail_last_page_len, what="tail")
+        if host_tail.numel() != host_indptr.numel():
+            raise ValueError("old and tail page tables must cover the same batch")
     batch = host_indptr.numel() - 1
     kind = {torch.int8: _capi.PG_KV_INT8, torch.float16: _capi.PG_KV_FP16,
             "heterogeneous": _capi.PG_KV_HETEROGENEOUS}[kv_data_type]
@@ -277,14 +335,14 @@ class BatchDecodeWithPagedKVCacheWrapper:
             raise ValueError("output must be float16")
         _check_index(indices, "indices")
         _check_index(last_page_len, "last_page_len")
-        host_indptr = _host_i32(indptr)
-        host_last = _host_i32(last_page_len)
+        host_indptr, host_last = _host_tables(indptr, last_page_len, indices)
         kind = _capi.PG_KV_INT8 if kv_dtype == torch.int8 else _capi.PG_KV_FP16
         split = 1 << 30 if disable_split_kv else (fixed_split_size or 0)
         self._state.make_plan(host_indptr, host_last, kind, None, None, num_qo_heads, num_kv_heads,
                               head_dim, page_size, split, 0, indices.device, num_cus)
         self._indices = indices
         self._last_page_len = last_page_len
+        self._id_range = _page_id_range(indices, host_indptr)
         self._kv_dtype = kv_dtype
         self._batch = host_indptr.numel() - 1
         self._num_qo_heads = num_qo_heads
@@ -320,6 +378,7 @@ class BatchDecodeWithPagedKVCacheWrapper:
         else:
             _check_cache(k_cache, "k_cache", torch.float16, self._num_kv_heads)
             _check_cache(v_cache, "v_cache", torch.float16, self._num_kv_heads)
+        _check_page_ids(self._id_range, min(k_cache.size(0), v_cache.size(0)), "KV")
         if out is None:
             out = torch.empty_like(q)
         if return_lse and lse is None:
@@ -385,16 +444,19 @@ class PageGaugeSegmentedDecode:
         for t, n in ((old_indices, "old_indices"), (old_last_page_len, "old_last_page_len"),
                      (tail_indices, "tail_indices"), (tail_last_page_len, "tail_last_page_len")):
             _check_index(t, n)
-        host_old = _host_i32(old_indptr)
-        host_tail = _host_i32(tail_indptr)
+        host_old, host_old_last = _host_tables(old_indptr, old_last_page_len, old_indices, "old")
+        host_tail, host_tail_last = _host_tables(tail_indptr, tail_last_page_len, tail_indices,
+                                                 "tail")
         if host_old.numel() != host_tail.numel():
             raise ValueError("old and tail page tables must cover the same batch")
-        self._state.make_plan(host_old, _host_i32(old_last_page_len), _capi.PG_KV_INT8, host_tail,
-                              _host_i32(tail_last_page_len), num_qo_heads, num_kv_heads, head_dim,
+        self._state.make_plan(host_old, host_old_last, _capi.PG_KV_INT8, host_tail,
+                              host_tail_last, num_qo_heads, num_kv_heads, head_dim,
                               page_size, fixed_split_size or 0, tail_split_size or 0,
                               old_indices.device, num_cus)
         self._old = (old_indices, old_last_page_len)
         self._tail = (tail_indices, tail_last_page_len)
+        self._id_ranges = (_page_id_range(old_indices, host_old),
+                           _page_id_range(tail_indices, host_tail))
         self._batch = host_old.numel() - 1
         self._num_qo_heads = num_qo_heads
         self._num_kv_heads = num_kv_heads
@@ -430,6 +492,8 @@ class PageGaugeSegmentedDecode:
         _check_scale(v_page_scale, "v_page_scale", v_codes.size(0), self._num_kv_heads)
         _check_cache(exact_k, "exact_k", torch.float16, self._num_kv_heads)
         _check_cache(exact_v, "exact_v", torch.float16, self._num_kv_heads)
+        _check_page_ids(self._id_ranges[0], min(k_codes.size(0), v_codes.size(0)), "INT8")
+        _check_page_ids(self._id_ranges[1], min(exact_k.size(0), exact_v.size(0)), "exact tail")
         center_stride = 0
         if value_center is not None:
             if (not value_center.is_cuda or value_center.dtype != torch.float16
@@ -555,13 +619,14 @@ class HeterogeneousDecodeWrapper:
             raise ValueError("the heterogeneous decode takes fp16 queries/outputs over int8 history")
         _check_index(indices, "indices")
         _check_index(last_page_len, "last_page_len")
-        host_indptr = _host_i32(indptr)
-        self._state.make_plan(host_indptr, _host_i32(last_page_len), _capi.PG_KV_HETEROGENEOUS,
+        host_indptr, host_last = _host_tables(indptr, last_page_len, indices)
+        self._state.make_plan(host_indptr, host_last, _capi.PG_KV_HETEROGENEOUS,
                               None, None, num_qo_heads, num_kv_heads, head_dim, page_size,
                               fixed_split_size or 0, 0, indices.device, num_cus,
                               exact_tail_pages_hint)
         self._indices = indices
         self._last_page_len = last_page_len
+        self._host_indptr = host_indptr
         self._batch = host_indptr.numel() - 1
         self._num_qo_heads = num_qo_heads
         self._num_kv_heads = num_kv_heads
@@ -574,6 +639,20 @@ class HeterogeneousDecodeWrapper:
     @property
     def num_work_items(self) -> int:
         return self._state.num_items
+
+    def _check_unified_page_ids(self, old_kv_len, code_pages: int, exact_pages: int) -> None:
+        """Opt-in bounds check of the unified table: entries below each
+        request's boundary index the code pool, the rest the exact pages.
+        Reads ``old_kv_len`` on the host (a synchronisation: debug only)."""
+        if not CHECK_PAGE_IDS:
+            return
+        ids = self._indices.detach().to("cpu")
+        boundary = old_kv_len.detach().to("cpu") // PAGE
+        for b in range(self._batch):
+            lo, hi = int(self._host_indptr[b]), int(self._host_indptr[b + 1])
+            cut = min(hi, lo + max(int(boundary[b]), 0))
+            _check_page_ids(_page_id_range(ids, torch.tensor([lo, cut])), code_pages, "INT8")
+            _check_page_ids(_page_id_range(ids, torch.tensor([cut, hi])), exact_pages, "exact")
 
     def run(self, q, paged_kv_cache, k_page_scale, v_page_scale, exact_k_cache, exact_v_cache,
             old_kv_len, value_center, sm_scale: Optional[float] = None, out=None, lse=None,
@@ -594,6 +673,8 @@ class HeterogeneousDecodeWrapper:
         _check_index(old_kv_len, "old_kv_len")
         if old_kv_len.numel() != self._batch:
             raise ValueError("old_kv_len must be contiguous CUDA [B] int32")
+        self._check_unified_page_ids(old_kv_len, min(old_k.size(0), old_v.size(0)),
+                                     min(exact_k_cache.size(0), exact_v_cache.size(0)))
         if (value_center.dtype != torch.float16 or not value_center.is_contiguous()
                 or tuple(value_center.shape) != (self._batch, self._num_kv_heads, DIM)):
             raise ValueError("value_center must be contiguous CUDA [B,Hkv,128] float16")

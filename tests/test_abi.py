@@ -88,7 +88,6 @@ def test_select_split_pages_fills_the_gpu():
     (dict(page_size=32), 3, "page size must be 16"),
     (dict(num_qo_heads=16), 3, "GQA group size 4"),
     (dict(last=[17]), 1, r"last_page_len must lie in \[1, 16\]"),
-    (dict(indptr=[5, 3]), 1, "indptr must be non-decreasing"),
 ])
 def test_host_plan_validation_messages(kwargs, code, message):
     from pagegauge_amd.decode import plan_work_items
@@ -99,6 +98,22 @@ def test_host_plan_validation_messages(kwargs, code, message):
         plan_work_items(args["indptr"], args["last"], num_qo_heads=args["num_qo_heads"],
                         head_dim=args["head_dim"], page_size=args["page_size"])
     assert f"(code {code})" in str(info.value)
+
+
+def test_c_planner_rejects_a_decreasing_indptr():
+    """The Python wrappers reject it first; the C planner checks it too."""
+    import ctypes
+
+    import torch
+
+    lib = _capi.library()
+    indptr = torch.tensor([5, 3], dtype=torch.int32)
+    last = torch.tensor([16], dtype=torch.int32)
+    plan = _capi.DecodePlan()
+    rc = lib.pg_decode_plan_host(indptr.data_ptr(), last.data_ptr(), 1, _capi.PG_KV_INT8, None,
+                                 None, 32, 8, 128, 16, 0, 0, 0, 256, ctypes.byref(plan), None, 0,
+                                 None)
+    assert rc == 1 and "indptr must be non-decreasing" in _capi.last_error()
 
 
 def test_missing_library_fails_loudly(monkeypatch, tmp_path):

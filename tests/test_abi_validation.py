@@ -174,3 +174,57 @@ def test_finalize_needs_int8_pages_and_positive_code_pages():
             FAKE, FAKE, FAKE, 1024, FAKE, FAKE, ctypes.c_float(0.088), FAKE, FAKE, 0, 0, None]
     rc, text = _call("pg_decode_run_finalize", *args)
     assert rc == 1 and "positive code pages per request" in text
+
+
+# --- host page tables checked before the planner reads them ----------------
+
+@pytest.mark.parametrize("indptr,last,message", [
+    ([0, 3, 5, 9], [16], "last_page_len must have one entry per request (3), got 1"),
+    ([0, 3, 5, 9], [16, 16, 16, 16], "one entry per request"),
+    ([-2, 3], [16], "indptr[0] must be non-negative"),
+    ([0, 5, 3], [16, 16], "indptr must be non-decreasing"),
+    ([0], [], "batch_size + 1 >= 2 entries"),
+])
+def test_plan_rejects_inconsistent_tables(indptr, last, message):
+    from pagegauge_amd import decode
+
+    with pytest.raises(ValueError, match=message.replace("(", r"\(").replace(")", r"\)")
+                       .replace("[", r"\[").replace("]", r"\]").replace("+", r"\+")):
+        decode.plan_work_items(indptr, last)
+
+
+def test_plan_rejects_a_short_tail_table():
+    from pagegauge_amd import decode
+
+    with pytest.raises(ValueError, match="tail last_page_len must have one entry per request"):
+        decode.plan_work_items([0, 3, 5], [16, 16], tail_indptr=[0, 1, 2], tail_last_page_len=[16])
+    with pytest.raises(ValueError, match="cover the same batch"):
+        decode.plan_work_items([0, 3, 5], [16, 16], tail_indptr=[0, 1], tail_last_page_len=[16])
+    with pytest.raises(ValueError, match="go together"):
+        decode.plan_work_items([0, 3], [16], tail_indptr=[0, 1])
+
+
+def test_host_tables_checks_the_indices_length():
+    from pagegauge_amd import decode
+
+    indices = torch.arange(8, dtype=torch.int32)
+    decode._host_tables([0, 3, 8], [16, 16], indices)           # exactly long enough
+    with pytest.raises(ValueError, match="indices has 8 entries but indptr\\[-1\\] is 9"):
+        decode._host_tables([0, 3, 9], [16, 16], indices)
+
+
+def test_page_id_check_is_opt_in(monkeypatch):
+    from pagegauge_amd import decode
+
+    ids = torch.tensor([4, 0, 7, 2], dtype=torch.int32)
+    indptr = torch.tensor([1, 3], dtype=torch.int32)          # planned ids: 0, 7
+    monkeypatch.setattr(decode, "CHECK_PAGE_IDS", False)
+    assert decode._page_id_range(ids, indptr) is None
+    monkeypatch.setattr(decode, "CHECK_PAGE_IDS", True)
+    span = decode._page_id_range(ids, indptr)
+    assert span == (0, 7)
+    decode._check_page_ids(span, 8, "INT8")
+    with pytest.raises(ValueError, match=r"INT8 page ids span \[0, 7\] but the pool holds 7 pages"):
+        decode._check_page_ids(span, 7, "INT8")
+    with pytest.raises(ValueError, match="span \\[-1, 3\\]"):
+        decode._check_page_ids((-1, 3), 8, "exact")

@@ -84,6 +84,35 @@ def test_medium_plans_with_long_items(cuda, workspace, lengths):
     assert max_abs(lse, ref_lse) <= LSE_TOL
 
 
+@pytest.mark.parametrize("flat,code", [("query", 127), ("query", -127), ("keys", 127)])
+def test_pv_digits_of_64_page_items_at_the_accumulator_bound(cuda, workspace, flat, code):
+    """Adversarial 64-page INT8 items (16 PV groups without a fold).
+
+    Equal scores (a zero query, or all-zero K codes) keep the running max
+    flat, so the PV accumulators sum all 16 groups before they are folded.
+    Every V code is +-127 and every V page scale is 1040/1024 * 2^-7: the
+    probability's fixed point is then 0x208000, whose middle radix-256
+    digit is -128 on every token, so the middle accumulator row reaches
+    16 * 64 * 128 * 127 = 16,646,144 in magnitude, and 256 times that passes
+    2^31.  The result must still match the oracle."""
+    from pagegauge_amd import workloads
+
+    w = workloads.build_decode_workload([2 * 64 * 16 + 256], seed=20260845, device=cuda)
+    if flat == "query":
+        w.query.zero_()
+    else:
+        w.k_codes.zero_()
+    w.v_codes.fill_(code)
+    w.v_scale.fill_(1040 / 1024 * 2 ** -7)
+    assert float(w.v_scale[0, 0]) == 1040 / 1024 * 2 ** -7
+    out, lse, dec = _segmented(w, workspace, split=64)
+    assert dec.split_pages == 64 and dec._state.plan.num_items_primary == 2
+    ref_out, ref_lse, _ = oracle_decode(w)
+    print("pv64", flat, code, max_abs(out, ref_out), flush=True)
+    assert max_abs(out, ref_out) <= OUT_TOL
+    assert max_abs(lse, ref_lse) <= LSE_TOL
+
+
 def test_b1_49k_config2_full_size(cuda, workspace):
     from pagegauge_amd import workloads
 
