@@ -192,6 +192,23 @@ int32_t pg_token_major_centers(const void* key, int64_t key_token_stride, const 
                                void* key_center, void* value_center, void* workspace,
                                int64_t workspace_bytes, void* stream);
 
+/* pg_token_major_centers without a workspace argument, for callers that
+ * cannot allocate (code under HIP graph capture, serving loops that forbid
+ * allocation).  It has no counterpart in the reference.  The chunk sums live
+ * in a file-scope device array of pg_token_major_centers_noalloc_max_bytes()
+ * bytes (8 MiB: ceil(tokens / 64) * heads <= 4096), one copy per GPU, held
+ * until the process ends; larger calls fail with PG_ERROR_WORKSPACE.  The
+ * call allocates nothing (no hipMalloc, hipFree or memset); the stream must
+ * belong to the current device.  Every call on a GPU shares that GPU's
+ * array: calls that overlap on one GPU (other streams, other threads) race
+ * and must be serialised by the caller.  Results are bit-identical to
+ * pg_token_major_centers. */
+int64_t pg_token_major_centers_noalloc_max_bytes(void);
+int32_t pg_token_major_centers_noalloc(const void* key, int64_t key_token_stride,
+                                       const void* value, int64_t value_token_stride,
+                                       int64_t tokens, int32_t heads, void* key_center,
+                                       void* value_center, void* stream);
+
 /* ------------------------------------------------------------------------
  * Paged decode (K1) and the split scheduler (S).
  * ---------------------------------------------------------------------- */

@@ -79,6 +79,8 @@ PROTOTYPES = {
                                      _i32, _p]),
     "pg_token_major_centers_workspace_bytes": (_i64, [_i64, _i32]),
     "pg_token_major_centers": (_i32, [_p, _i64, _p, _i64, _i64, _i32, _p, _p, _p, _i64, _p]),
+    "pg_token_major_centers_noalloc_max_bytes": (_i64, []),
+    "pg_token_major_centers_noalloc": (_i32, [_p, _i64, _p, _i64, _i64, _i32, _p, _p, _p]),
     "pg_decode_workspace_bytes": (_i64, [_i32, _i32, _i64, _i64]),
     "pg_select_split_pages": (_i32, [_i64, _i32, _i32, _i32, _i32]),
     "pg_decode_plan": (_i32, [_p, _p, _i32, _i32, _p, _p, _i32, _i32, _i32, _i32, _i32, _i32,

@@ -18,6 +18,8 @@
 
 #include "pg_common.h"
 
+#include <mutex>
+
 namespace pg {
 namespace {
 
@@ -816,24 +818,26 @@ extern "C" int64_t pg_token_major_centers_workspace_bytes(int64_t tokens, int32_
   return 2 * chunks * heads * kHeadDim * static_cast<int64_t>(sizeof(int64_t));
 }
 
-extern "C" int32_t pg_token_major_centers(const void* key, int64_t key_token_stride,
-                                          const void* value, int64_t value_token_stride,
-                                          int64_t tokens, int32_t heads, void* key_center,
-                                          void* value_center, void* workspace,
-                                          int64_t workspace_bytes, void* stream) {
-  clear_error();
+namespace {
+
+// Both center entry points: checks, then the chunk-sum and finalize launches
+// with the chunk sums in ``partial`` (2 * chunks * heads * 128 int64).
+int32_t launch_centers(const void* key, int64_t key_token_stride, const void* value,
+                       int64_t value_token_stride, int64_t tokens, int32_t heads,
+                       void* key_center, void* value_center, int64_t* partial,
+                       int64_t partial_bytes, hipStream_t stream) {
   if (tokens <= 0 || heads <= 0)
     return fail(PG_ERROR_INVALID_ARGUMENT, "token-major K/V must contain tokens and heads");
   if (tokens > kCenterMaxTokens)
     return fail(PG_ERROR_INVALID_ARGUMENT, "at most 4194304 tokens per center reduction");
-  if (any_null({key, value, key_center, value_center, workspace}))
+  if (any_null({key, value, key_center, value_center, partial}))
     return fail(PG_ERROR_INVALID_ARGUMENT, "null tensor pointer");
   const int64_t row = static_cast<int64_t>(heads) * kHeadDim;
   if (key_token_stride < row || value_token_stride < row || key_token_stride % 2 ||
       value_token_stride % 2)
     return fail(PG_ERROR_INVALID_ARGUMENT,
                 "token strides must be even and cover heads*128 elements");
-  if (workspace_bytes < pg_token_major_centers_workspace_bytes(tokens, heads))
+  if (partial_bytes < pg_token_major_centers_workspace_bytes(tokens, heads))
     return fail(PG_ERROR_WORKSPACE, "center workspace too small");
   CenterParams p{};
   p.source[0] = static_cast<const uint16_t*>(key);
@@ -842,17 +846,101 @@ extern "C" int32_t pg_token_major_centers(const void* key, int64_t key_token_str
   p.token_stride[1] = value_token_stride;
   p.center[0] = static_cast<uint16_t*>(key_center);
   p.center[1] = static_cast<uint16_t*>(value_center);
-  p.partial = static_cast<int64_t*>(workspace);
+  p.partial = partial;
   p.tokens = tokens;
   p.columns = static_cast<int>(row);
   p.chunks = static_cast<int>((tokens + kCenterChunk - 1) / kCenterChunk);
   const unsigned column_blocks = static_cast<unsigned>((row / 2 + kCenterThreads - 1) / kCenterThreads);
   hipLaunchKernelGGL(center_partial_kernel, dim3(column_blocks, p.chunks, 2), dim3(kCenterThreads),
-                     0, as_stream(stream), p);
+                     0, stream, p);
   int32_t rc = check_launch("token_major_centers");
   if (rc != PG_OK) return rc;
   const unsigned finalize_blocks = static_cast<unsigned>((row + kCenterThreads - 1) / kCenterThreads);
   hipLaunchKernelGGL(center_finalize_kernel, dim3(finalize_blocks, 2), dim3(kCenterThreads), 0,
-                     as_stream(stream), p);
+                     stream, p);
   return check_launch("token_major_centers");
+}
+
+}  // namespace
+
+extern "C" int32_t pg_token_major_centers(const void* key, int64_t key_token_stride,
+                                          const void* value, int64_t value_token_stride,
+                                          int64_t tokens, int32_t heads, void* key_center,
+                                          void* value_center, void* workspace,
+                                          int64_t workspace_bytes, void* stream) {
+  clear_error();
+  return launch_centers(key, key_token_stride, value, value_token_stride, tokens, heads,
+                        key_center, value_center, static_cast<int64_t*>(workspace),
+                        workspace_bytes, as_stream(stream));
+}
+
+// ---------------------------------------------------------------------------
+// No-allocation variant: the chunk sums live in ``scratch``, a file-scope
+// device array.  Every GPU the library runs on holds its own copy (8 MiB)
+// until the process ends.  On the host, ``scratch`` names a host-side stand-in,
+// not device memory: the device address of each GPU's copy comes from
+// hipGetSymbolAddress, taken once per device with that device current, and
+// only that address is ever handed to a kernel.
+// ---------------------------------------------------------------------------
+namespace pg {
+namespace {
+
+constexpr int64_t kCenterScratchBytes = int64_t{8} << 20;
+static __device__ __align__(256) int64_t scratch[kCenterScratchBytes / sizeof(int64_t)];
+
+constexpr int kMaxScratchDevices = 64;
+std::mutex g_scratch_mutex;
+void* g_scratch_address[kMaxScratchDevices] = {};
+
+// Device address of this GPU's ``scratch`` (the current device, which must
+// be the stream's).
+int32_t center_scratch(hipStream_t stream, int64_t** address) {
+  int device = -1;
+  if (hipGetDevice(&device) != hipSuccess)
+    return fail(PG_ERROR_LAUNCH, "hipGetDevice failed");
+  if (stream != nullptr) {
+    int stream_device = -1;
+    if (hipStreamGetDevice(stream, &stream_device) != hipSuccess)
+      return fail(PG_ERROR_INVALID_ARGUMENT, "hipStreamGetDevice failed");
+    if (stream_device != device)
+      return fail(PG_ERROR_INVALID_ARGUMENT,
+                  "the stream belongs to another device than the current one");
+  }
+  if (device < 0 || device >= kMaxScratchDevices)
+    return fail(PG_ERROR_UNSUPPORTED, "device ordinal beyond the scratch table");
+  std::lock_guard<std::mutex> lock(g_scratch_mutex);
+  if (g_scratch_address[device] == nullptr) {
+    void* ptr = nullptr;
+    const hipError_t status = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (status != hipSuccess || ptr == nullptr)
+      return fail(PG_ERROR_LAUNCH, std::string("hipGetSymbolAddress(scratch) failed: ") +
+                                       hipGetErrorString(status));
+    g_scratch_address[device] = ptr;
+  }
+  *address = static_cast<int64_t*>(g_scratch_address[device]);
+  return PG_OK;
+}
+
+}  // namespace
+}  // namespace pg
+
+extern "C" int64_t pg_token_major_centers_noalloc_max_bytes(void) { return kCenterScratchBytes; }
+
+extern "C" int32_t pg_token_major_centers_noalloc(const void* key, int64_t key_token_stride,
+                                                  const void* value, int64_t value_token_stride,
+                                                  int64_t tokens, int32_t heads,
+                                                  void* key_center, void* value_center,
+                                                  void* stream) {
+  clear_error();
+  const int64_t need = pg_token_major_centers_workspace_bytes(tokens, heads);
+  if (need > kCenterScratchBytes)
+    return fail(PG_ERROR_WORKSPACE,
+                "the no-allocation center reduction holds at most 8 MiB of chunk sums "
+                "(tokens/64 rounded up x heads <= 4096); this call needs " +
+                    std::to_string(need) + " bytes");
+  int64_t* partial = nullptr;
+  if (int32_t rc = center_scratch(as_stream(stream), &partial)) return rc;
+  return launch_centers(key, key_token_stride, value, value_token_stride, tokens, heads,
+                        key_center, value_center, partial, kCenterScratchBytes,
+                        as_stream(stream));
 }
