@@ -158,6 +158,15 @@ int32_t pg_quantize_completed_kv_pages(const void* key, const void* value,
                                        void* key_scales, void* value_scales,
                                        int64_t num_pages, int32_t heads, void* stream);
 
+/* The K1 driver's page quantizer quantize_page_gauge
+ * (scripts/benchmark_flashinfer_page_affine_int8.py:256-278) given its
+ * center: values [pages,16,H,128] fp16, center [H,128] fp16; float32-centered
+ * values, scale fp16(max(amax/127, 2^-20)) per (page, head) into scales
+ * [pages,H], codes round-half-even(x / scale) clamped to [-127, 127] (torch's
+ * round) into codes [pages,16,H,128] int8.  One tensor per call. */
+int32_t pg_quantize_page_gauge(const void* values, const void* center, int8_t* codes,
+                               void* scales, int64_t num_pages, int32_t heads, void* stream);
+
 /* Prefill cache population of one (layer, request): the bulk quantizer above
  * plus the centered FP16 exact pages, in one launch.  Replaces the body of
  * populate_backend_cache_layer (diagnostics/benchmark_backend_exclusive.py:442-506)

@@ -75,6 +75,7 @@ PROTOTYPES = {
     "pg_append_finalize_page_gauge": (_i32, [_p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _i32,
                                              _i32, _i32, _p]),
     "pg_quantize_completed_kv_pages": (_i32, [_p, _p, _p, _p, _p, _p, _p, _p, _i64, _i32, _p]),
+    "pg_quantize_page_gauge": (_i32, [_p, _p, _p, _p, _i64, _i32, _p]),
     "pg_prefill_page_gauge": (_i32, [_p, _i64, _p, _i64, _p, _p, _p, _p, _p, _p, _p, _p, _p, _i64,
                                      _i32, _p]),
     "pg_token_major_centers_workspace_bytes": (_i64, [_i64, _i32]),

@@ -299,7 +299,10 @@ __global__ __launch_bounds__(kWave * kWavesPerBlock) void paged_append_kernel(Pa
 
 // Bulk quantizer: one wave per (page, head); float32-centered values (not
 // rounded to FP16), scale and sign-symmetric codes as the finalize
-// (scripts/benchmark_page_gauge_overheads.py:23-83).
+// (scripts/benchmark_page_gauge_overheads.py:23-83), or with ``half_even``
+// the round-half-even codes of the K1 driver's quantize_page_gauge
+// (scripts/benchmark_flashinfer_page_affine_int8.py:256-278: torch.round of
+// the float32 quotient).  ``value`` may be null (one tensor).
 struct QuantizeParams {
   const uint16_t* key;
   const uint16_t* value;
@@ -318,7 +321,14 @@ struct QuantizeParams {
   const int32_t* exact_map;
   uint16_t* exact_key;
   uint16_t* exact_value;
+  int half_even;
 };
+
+// Round-half-even of the quotient (v_rndne_f32 under the default rounding
+// mode), clamped to [-127, 127].
+__device__ __forceinline__ int8_t half_even_code(float quotient) {
+  return static_cast<int8_t>(fminf(fmaxf(rintf(quotient), -127.0f), 127.0f));
+}
 
 // ``src`` rows are ``src_stride`` elements apart, code rows ``row_stride``.
 // With ``ring`` set, the FP16-rounded centered rows are also written there
@@ -326,7 +336,7 @@ struct QuantizeParams {
 __device__ __forceinline__ void quantize_block(const uint16_t* src, int64_t src_stride,
                                                const uint16_t* center, int64_t row_stride,
                                                int8_t* codes, uint16_t* scale_out,
-                                               uint16_t* ring, int lane) {
+                                               uint16_t* ring, int lane, bool half_even) {
   const Half2Bits c = load_pair(center + 2 * lane);
   const float c0 = half_bits_to_float(c.lo);
   const float c1 = half_bits_to_float(c.hi);
@@ -349,8 +359,10 @@ __device__ __forceinline__ void quantize_block(const uint16_t* src, int64_t src_
   const float scale = half_bits_to_float(scale_bits);
 #pragma unroll
   for (int t = 0; t < kPageSize; ++t) {
-    const int8_t q0 = sign_symmetric_code(lo[t] / scale);
-    const int8_t q1 = sign_symmetric_code(hi[t] / scale);
+    const float d0 = lo[t] / scale;
+    const float d1 = hi[t] / scale;
+    const int8_t q0 = half_even ? half_even_code(d0) : sign_symmetric_code(d0);
+    const int8_t q1 = half_even ? half_even_code(d1) : sign_symmetric_code(d1);
     *reinterpret_cast<uint16_t*>(codes + t * row_stride + 2 * lane) =
         static_cast<uint16_t>(static_cast<uint8_t>(q0)) |
         static_cast<uint16_t>(static_cast<uint16_t>(static_cast<uint8_t>(q1)) << 8);
@@ -370,11 +382,12 @@ __global__ __launch_bounds__(kWave * kWavesPerBlock) void quantize_pages_kernel(
   quantize_block(p.key + page * kPageSize * p.key_token_stride + head * kHeadDim,
                  p.key_token_stride, p.key_center + head * kHeadDim, row_stride,
                  p.key_codes + base, p.key_scales + item,
-                 ring_page >= 0 ? p.exact_key + ring_base : nullptr, lane);
-  quantize_block(p.value + page * kPageSize * p.value_token_stride + head * kHeadDim,
-                 p.value_token_stride, p.value_center + head * kHeadDim, row_stride,
-                 p.value_codes + base, p.value_scales + item,
-                 ring_page >= 0 ? p.exact_value + ring_base : nullptr, lane);
+                 ring_page >= 0 ? p.exact_key + ring_base : nullptr, lane, p.half_even != 0);
+  if (p.value != nullptr)
+    quantize_block(p.value + page * kPageSize * p.value_token_stride + head * kHeadDim,
+                   p.value_token_stride, p.value_center + head * kHeadDim, row_stride,
+                   p.value_codes + base, p.value_scales + item,
+                   ring_page >= 0 ? p.exact_value + ring_base : nullptr, lane, p.half_even != 0);
 }
 
 // Exact per-(head, dim) token mean.  Every FP16 value is an integer multiple
@@ -770,6 +783,26 @@ extern "C" int32_t pg_quantize_completed_kv_pages(const void* key, const void* v
   p.heads = heads;
   p.key_token_stride = p.value_token_stride = static_cast<int64_t>(heads) * kHeadDim;
   return launch_quantize(p, as_stream(stream), "quantize_completed_kv_pages");
+}
+
+extern "C" int32_t pg_quantize_page_gauge(const void* values, const void* center,
+                                          int8_t* codes, void* scales, int64_t num_pages,
+                                          int32_t heads, void* stream) {
+  clear_error();
+  if (num_pages <= 0 || heads <= 0)
+    return fail(PG_ERROR_INVALID_ARGUMENT, "pages and heads must be positive");
+  if (any_null({values, center, codes, scales}))
+    return fail(PG_ERROR_INVALID_ARGUMENT, "null tensor pointer");
+  QuantizeParams p{};
+  p.key = static_cast<const uint16_t*>(values);
+  p.key_center = static_cast<const uint16_t*>(center);
+  p.key_codes = codes;
+  p.key_scales = static_cast<uint16_t*>(scales);
+  p.num_pages = num_pages;
+  p.heads = heads;
+  p.key_token_stride = static_cast<int64_t>(heads) * kHeadDim;
+  p.half_even = 1;
+  return launch_quantize(p, as_stream(stream), "quantize_page_gauge");
 }
 
 extern "C" int32_t pg_prefill_page_gauge(const void* key, int64_t key_token_stride,

@@ -49,6 +49,40 @@ def quantize_completed_kv_pages(key, value, key_center, value_center, key_codes,
                key.shape[2], _stream())
 
 
+def quantize_page_gauge(values: torch.Tensor, center: torch.Tensor | None = None):
+    """The K1 driver's quantizer (scripts/benchmark_flashinfer_page_affine_int8.py:256-278).
+
+    ``values`` [pages, 16, H, 128] fp16 on the GPU.  Returns ``(codes, center,
+    scale, reconstructed_centered, centered)`` like the reference:
+    * center: the per-(head, dim) mean over every page and token, as FP16
+      (``token_major_centers``: the exact mean; the reference's float32
+      ``mean`` agrees except where its own rounding crosses a half-ulp
+      boundary), unless given;
+    * codes and scale from ``pg_quantize_page_gauge``: float32-centered values,
+      scale fp16(max(amax/127, 2^-20)) per (page, head), round-half-even codes;
+    * reconstructed_centered = fp16(codes * scale), centered = fp16(values -
+      center) (element-wise, as the reference returns them).
+    """
+    if values.ndim != 4 or values.shape[1] != PAGE or values.shape[3] != DIM:
+        raise ValueError("values must be [pages, 16, HKV, 128]")
+    if values.dtype != torch.float16:
+        raise ValueError("values must be float16")
+    pages, heads = int(values.shape[0]), int(values.shape[2])
+    if center is None:
+        flat = values.view(pages * PAGE, heads, DIM)
+        center = token_major_centers(flat, flat)[0]
+    if tuple(center.shape) != (heads, DIM) or center.dtype != torch.float16:
+        raise ValueError("center must be float16 [heads, 128]")
+    _all_cuda_contiguous(values, center)
+    codes = torch.empty(values.shape, dtype=torch.int8, device=values.device)
+    scale = torch.empty(pages, heads, dtype=torch.float16, device=values.device)
+    _capi.call("pg_quantize_page_gauge", values.data_ptr(), center.data_ptr(), codes.data_ptr(),
+               scale.data_ptr(), pages, heads, _stream())
+    reconstructed = (codes.float() * scale.float()[:, None, :, None]).half()
+    centered = (values.float() - center.float()[None, None]).half()
+    return codes, center, scale, reconstructed, centered
+
+
 def _check_ids(key, page_ids, page_offsets) -> None:
     if page_ids.shape != (key.shape[0],) or page_offsets.shape != page_ids.shape:
         raise ValueError("page IDs and offsets must have one entry per request")

@@ -1,12 +1,16 @@
 """Synthetic decode workloads of the benchmark configurations.
 
 Seeded inputs are generated on the CPU with ``torch.Generator`` (so the same
-seed gives the same tensors on any machine), then copied to the device.  INT8
-history pages are produced by this package's own bulk quantizer
-(``pg_quantize_completed_kv_pages``) from centered K/V, exactly as a real
-cache is built at prefill; the newest ``tail_tokens`` tokens are kept as a
-centered FP16 ring.  Physical page ids are a seeded random permutation of a
-shared pool.
+seed gives the same tensors on any machine), then copied to the device.  Each
+request's channel centers are the exact token mean of its whole context
+(``token_major_centers``), and its INT8 history pages are quantised on the GPU
+as the reference's K1 driver builds its caches (``quantize_page_gauge``,
+scripts/benchmark_flashinfer_page_affine_int8.py:256-278 and :489-494:
+float32-centered values, round-half-even codes), or with
+``quantizer="completed_pages"`` by the prefill bulk quantizer
+(``pg_quantize_completed_kv_pages``: sign-symmetric rounding); the newest
+``tail_tokens`` tokens are kept as a centered FP16 ring.  Physical page ids are
+a seeded random permutation of a shared pool.
 
 Configurations (shapes of the reference's Mistral-7B layer: 32 query heads,
 8 KV heads, head_dim 128, 16-token pages):
@@ -24,7 +28,7 @@ from typing import Optional, Sequence
 
 import torch
 
-from .update import quantize_completed_kv_pages
+from .update import quantize_completed_kv_pages, quantize_page_gauge, token_major_centers
 
 HQ = 32
 HKV = 8
@@ -101,7 +105,8 @@ def _outlier_kv(generator: torch.Generator, tokens: int, outlier_channels: int,
 def build_decode_workload(lengths: Sequence[int], seed: int, device="cuda",
                           tail_tokens: int = TAIL_TOKENS, outlier_channels: int = 4,
                           outlier_gain: float = 8.0, shuffle_pages: bool = True,
-                          with_fp16_copy: bool = False, query_scale: float = 1.0) -> DecodeWorkload:
+                          with_fp16_copy: bool = False, query_scale: float = 1.0,
+                          quantizer: str = "page_gauge") -> DecodeWorkload:
     """Build a seeded INT8-history + FP16-tail workload for ``lengths``.
 
     Each length must be a positive multiple of 16 and larger than
@@ -112,6 +117,8 @@ def build_decode_workload(lengths: Sequence[int], seed: int, device="cuda",
         raise ValueError("lengths must be multiples of 16 longer than the tail")
     if tail_tokens % PAGE:
         raise ValueError("tail must be whole pages")
+    if quantizer not in ("page_gauge", "completed_pages"):
+        raise ValueError("quantizer must be 'page_gauge' or 'completed_pages'")
     generator = torch.Generator().manual_seed(seed)
     batch = len(lengths)
     query = (torch.randn(batch, HQ, DIM, generator=generator) * query_scale).to(torch.float16)
@@ -143,11 +150,6 @@ def build_decode_workload(lengths: Sequence[int], seed: int, device="cuda",
     for request, length in enumerate(lengths):
         keys = _outlier_kv(generator, length, outlier_channels, outlier_gain)
         values = _outlier_kv(generator, length, outlier_channels, outlier_gain)
-        # per-(request, kv head) channel center over the whole context
-        kc = keys.float().mean(dim=0).to(torch.float16)
-        vc = values.float().mean(dim=0).to(torch.float16)
-        key_centers.append(kc)
-        value_centers.append(vc)
         n_old = old_counts[request]
         ids_old = old_perm[old_cursor:old_cursor + n_old]
         ids_tail = tail_perm[tail_cursor:tail_cursor + tail_pages]
@@ -157,15 +159,22 @@ def build_decode_workload(lengths: Sequence[int], seed: int, device="cuda",
         tail_indices.append(ids_tail)
         dev_k = keys.reshape(-1, PAGE, HKV, DIM).to(device)
         dev_v = values.reshape(-1, PAGE, HKV, DIM).to(device)
-        dkc, dvc = kc.to(device), vc.to(device)
-        # history: bulk quantizer into the shuffled pool
+        # per-(request, kv head) channel centers: exact mean of the whole context
+        dkc, dvc = token_major_centers(dev_k.view(-1, HKV, DIM), dev_v.view(-1, HKV, DIM))
+        key_centers.append(dkc)
+        value_centers.append(dvc)
+        # history: quantised into the shuffled pool
         old_k = dev_k[:n_old].contiguous()
         old_v = dev_v[:n_old].contiguous()
-        ck = torch.empty(n_old, PAGE, HKV, DIM, dtype=torch.int8, device=device)
-        cv = torch.empty_like(ck)
-        sk = torch.empty(n_old, HKV, dtype=torch.float16, device=device)
-        sv = torch.empty_like(sk)
-        quantize_completed_kv_pages(old_k, old_v, dkc, dvc, ck, cv, sk, sv)
+        if quantizer == "page_gauge":
+            ck, _, sk, _, _ = quantize_page_gauge(old_k, dkc)
+            cv, _, sv, _, _ = quantize_page_gauge(old_v, dvc)
+        else:
+            ck = torch.empty(n_old, PAGE, HKV, DIM, dtype=torch.int8, device=device)
+            cv = torch.empty_like(ck)
+            sk = torch.empty(n_old, HKV, dtype=torch.float16, device=device)
+            sv = torch.empty_like(sk)
+            quantize_completed_kv_pages(old_k, old_v, dkc, dvc, ck, cv, sk, sv)
         dev_ids = ids_old.to(device)
         k_codes[dev_ids] = ck
         v_codes[dev_ids] = cv
@@ -204,7 +213,7 @@ def build_decode_workload(lengths: Sequence[int], seed: int, device="cuda",
         key_center=torch.stack(key_centers).to(device),
         value_center=torch.stack(value_centers).to(device),
         meta={"seed": seed, "outlier_channels": outlier_channels, "outlier_gain": outlier_gain,
-              "tail_tokens": tail_tokens, "shuffled": shuffle_pages},
+              "tail_tokens": tail_tokens, "shuffled": shuffle_pages, "quantizer": quantizer},
     )
     if with_fp16_copy:
         workload.fp16_k = fp16_k

@@ -40,3 +40,80 @@ def max_abs(a, b) -> float:
     a = cpu(a) if not isinstance(a, np.ndarray) else a
     b = cpu(b) if not isinstance(b, np.ndarray) else b
     return float(np.abs(a.astype(np.float64) - b.astype(np.float64)).max())
+
+
+def dense_reference_class(dec, dtype=None, attention_output="kernel"):
+    """A ``dec.PageGaugeDecoder`` whose attention is the dense softmax, in
+    ``dtype`` (float32 by default), over the reconstructed cache: K = c_K +
+    s*Z for old pages and c_K + ring for tail pages, V likewise, from the same
+    cache the K2 kernel updates (the reference's explicit-reconstruction path,
+    diagnostics/benchmark_heterogeneous_fa2_correctness.py:291-299).  The
+    PageGauge kernel runs on the same inputs first (it also finalizes a page
+    that the step's token completes); ``kernel_error`` records max |kernel -
+    dense| minus half an FP16 ulp of the dense value (the kernel's output
+    rounding).  One request (batch 1).
+
+    ``attention_output``: "kernel" feeds the FP16-rounded dense attention to
+    the decoder's own O projection; "float16" and "float32" instead run the O
+    projection as one float32 torch product of the FP16-rounded, or unrounded,
+    dense attention (same epilogue: the projection rounded to FP16, then the
+    FP16 residual add).  The two differ only by the FP16 rounding of the
+    attention output, which measures the decoder's rounding floor."""
+    import math
+
+    import torch
+
+    dtype = torch.float32 if dtype is None else dtype
+
+    class DenseReference(dec.PageGaugeDecoder):
+        kernel_error = 0.0
+
+        def attention(self, layer):
+            kernel = super().attention(layer).float().clone()
+            dense = self._dense(layer)
+            excess = (kernel.to(dtype) - dense).abs() - dense.abs() * 2.0 ** -11
+            self.kernel_error = max(self.kernel_error, float(excess.max()))
+            self.last_dense = dense
+            self.attention_output[layer].copy_(dense.to(torch.float16))
+            return self.attention_output[layer]
+
+        def _layer_fused(self, layer):
+            if attention_output == "kernel":
+                return super()._layer_fused(layer)
+            if not self.fused_append:
+                raise ValueError("the float O projection reference runs the fused cache update")
+            cfg = self.config
+            w = self.weights.layers[layer]
+            qw = cfg.q_heads * 128
+            self._qkv_append(layer)
+            self.attention(layer)
+            a = self.last_dense.float()
+            if attention_output == "float16":
+                a = a.half().float()
+            proj = torch.matmul(a.view(self.batch_size, qw), w["o"].float().t())
+            self._hidden.copy_(self._hidden + proj.half())
+            dec.projection(w["gate_up"], self._hidden, self._activation,
+                           norm_weight=w["post_norm"], eps=cfg.rms_eps, swiglu=True)
+            dec.projection(w["down"], self._activation, self._hidden, residual=self._hidden)
+
+        def _dense(self, layer):
+            c = self.cache
+            b = 0
+            old = self.old_table.active_indices().long()
+            tail = self.exact_table.active_indices().long()
+            last = int(self.exact_table.host_last_len[b])
+            kc = c.key_center[layer, b].to(dtype)
+            vc = c.value_center[layer, b].to(dtype)
+            k_old = c.key_codes[layer][old].to(dtype) * c.key_scales[layer][old].to(dtype)[:, None, :, None]
+            v_old = c.value_codes[layer][old].to(dtype) * c.value_scales[layer][old].to(dtype)[:, None, :, None]
+            k_tail = c.exact_key[layer][tail].to(dtype)
+            v_tail = c.exact_value[layer][tail].to(dtype)
+            n_tail = (tail.numel() - 1) * 16 + last
+            keys = torch.cat((k_old.reshape(-1, 8, 128), k_tail.reshape(-1, 8, 128)[:n_tail])) + kc
+            values = torch.cat((v_old.reshape(-1, 8, 128), v_tail.reshape(-1, 8, 128)[:n_tail])) + vc
+            q = self.rotated_query[b].to(dtype).view(8, 4, 128)
+            scores = torch.matmul(q, keys.permute(1, 2, 0).contiguous()) / math.sqrt(128)
+            probs = torch.softmax(scores, dim=-1)
+            return torch.matmul(probs, values.permute(1, 0, 2).contiguous()).reshape(1, 32, 128)
+
+    return DenseReference

@@ -339,3 +339,40 @@ def test_paged_append_and_finalize_bit_exact(cuda):
     for name, got, want in zip(["exact_k", "exact_v", "codes_k", "codes_v", "scales_k", "scales_v"],
                                state, host):
         assert_bit_equal(got, want, name)
+
+
+def test_page_gauge_quantizer_bit_exact(cuda):
+    """a13: the K1 driver's quantize_page_gauge on the GPU (round-half-even
+    codes of the float32-centered values), bit-exact against the oracle given
+    the center, and the center equal to the oracle's exact mean.  Page 0 holds
+    exact half-way quotients (k + 1/2 with scale 1/8), where half-even and the
+    finalize's sign-symmetric rounding disagree for even k; page 1 is all zero
+    (the 2^-20 scale floor)."""
+    from pagegauge_amd import update
+
+    gen = torch.Generator().manual_seed(20260814)
+    pages, heads = 41, 8
+    values = _rand(gen, pages, 16, heads, 128, scale=2.0)
+    ladder = (torch.arange(16 * 128, dtype=torch.float32).reshape(16, 128) % 127 + 0.5) / 8
+    ladder[0, 0] = 127 / 8                     # page max: scale = 127/8 / 127 = 1/8 exactly
+    sign = torch.where(torch.arange(128) % 2 == 0, 1.0, -1.0)
+    values[0] = (ladder * sign).half()[:, None, :].expand(16, heads, 128)
+    values[1] = 0
+    zero = torch.zeros(heads, 128, dtype=torch.float16)
+    codes, center, scale, recon, centered = update.quantize_page_gauge(values.to(cuda), zero.to(cuda))
+    torch.cuda.synchronize()
+    want = oracle.quantize_page_gauge(values.numpy(), zero.numpy())
+    for name, got, ref in zip(["codes", "center", "scale", "reconstructed", "centered"],
+                              (codes, center, scale, recon, centered), want):
+        assert_bit_equal(got, ref, name)
+    assert float(scale[0, 0]) == 0.125
+    ties = cpu(codes)[0, :, 0, :].astype(np.int32)
+    half_away = np.sign(ladder.numpy() * sign.numpy()) * np.floor(np.abs(ladder.numpy() * 8 * sign.numpy()) + 0.5)
+    assert (ties != half_away).any()            # the tie page does tell the two roundings apart
+    # the center computed on the GPU (exact token mean) as the reference's center
+    codes2, center2, scale2, _, _ = update.quantize_page_gauge(values.to(cuda))
+    torch.cuda.synchronize()
+    want2 = oracle.quantize_page_gauge(values.numpy())
+    assert_bit_equal(center2, want2[1], "center")
+    assert_bit_equal(codes2, want2[0], "codes")
+    assert_bit_equal(scale2, want2[2], "scale")
