@@ -75,7 +75,7 @@ def test_served_batch_matches_the_oracle_step_by_step(cuda):
     ext = load_append_extension()
     gen = torch.Generator().manual_seed(20260860)
     pol = sv.Policy(prefix_pages=2, suffix_pages=4, tail_pages=3)
-    slots = sv.RequestSlots(3, pol)
+    ledger = sv.Ledger(3, pol)
     n_pages = 320
     pool = Pool(n_pages, gen)
     d = {"codes_k": torch.zeros(n_pages, PAGE, HKV, D, device=cuda, dtype=torch.int8),
@@ -89,7 +89,7 @@ def test_served_batch_matches_the_oracle_step_by_step(cuda):
 
     def admit(name, prompt):
         table = pool.take((prompt + PAGE - 1) // PAGE)
-        lease = slots.admit(name, prompt, table)
+        lease = ledger.admit(name, prompt, table, ready=True)
         tables[name] = table
         _prefill(d, lease, prompt, table, gen, pol, cuda)
         return lease
@@ -105,7 +105,7 @@ def test_served_batch_matches_the_oracle_step_by_step(cuda):
             for key in cache_keys:
                 assert_bit_equal(d[key], mirror[key], f"{key} before the retirement")
             retired = tables.pop("a")
-            slots.release(leases.pop("a"))
+            ledger.release(leases.pop("a"))
             pool.give(retired)
             leases["d"] = admit("d", 904)
             assert leases["d"].slot == 0 and leases["d"].generation == 2
@@ -115,11 +115,11 @@ def test_served_batch_matches_the_oracle_step_by_step(cuda):
                 mirror[k] = cpu(d[k]).copy()
         scheduled = []
         for name, lease in leases.items():
-            position = slots.state(lease).current_tokens
+            position = ledger.view(lease).current_tokens
             if position % PAGE == 0:
                 tables[name] = tables[name] + pool.take(1)
             scheduled.append((lease, position, tables[name]))
-        batch = sv.prepare_decode(slots, scheduled)
+        batch = ledger.stage_decode(scheduled)
         t = sv.decode_tables(batch, pol, device=cuda)
         read_back |= finalized & set(cpu(t.old_indices).tolist())
         finalized |= {table[position // PAGE] for _, position, table in scheduled
@@ -157,7 +157,7 @@ def test_served_batch_matches_the_oracle_step_by_step(cuda):
         worst = max(worst, max_abs(out, want))
         assert max_abs(out, want) <= 2e-3, step
         assert max_abs(lse, want_lse) <= 2e-3, step
-        sv.commit_decode(slots, batch)
+        ledger.commit_decode(batch)
     print(f"served decode: 64 steps, max |out - oracle| = {worst:.3g}, "
           f"{len(read_back)} decode-finalized pages read back as INT8 history")
     for key in cache_keys:

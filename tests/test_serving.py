@@ -1,5 +1,6 @@
-"""Serving metadata on the CPU: the S/A/T partition, exact slots, request
-leases, decode-batch metadata, device tables and pool accounting.
+"""Serving metadata on the CPU: the S/A/T partition, exact slots, the
+ledger's slot state machine and page ownership, staged decode steps, device
+tables and pool accounting.
 
 Expectations follow the reference's serving prototype
 (experiments/mlsys2027/serving_v1/pagegauge_vllm/, pinned by
@@ -67,41 +68,50 @@ def test_exact_slot_layout():
         sv.exact_slot(-1, 4096, 0, pol)
 
 
-def test_request_slot_lifecycle_and_generations():
-    slots = sv.RequestSlots(2)
-    a = slots.admit("a", 4096, range(256))
-    b = slots.admit("b", 4096, range(256, 512))
+def _append(ledger, lease, position, table):
+    """Stage and commit one token of one request."""
+    return ledger.commit_decode(ledger.stage_decode([(lease, position, table)]))[0]
+
+
+def test_ledger_slots_and_generations():
+    ledger = sv.Ledger(2)
+    a = ledger.admit("a", 4096, range(256), ready=True)
+    b = ledger.admit("b", 4096, range(256, 512), ready=True)
     assert (a.slot, a.generation, b.slot) == (0, 1, 1)
     with pytest.raises(MemoryError, match="admission capacity"):
-        slots.admit("c", 4096, range(512, 768))
+        ledger.admit("c", 4096, range(512, 768))
     with pytest.raises(ValueError, match="duplicate live request"):
-        slots.admit("a", 4096, range(800, 1056))
-    info = slots.append(a, 4096, list(range(256)) + [900])
+        ledger.admit("a", 4096, range(800, 1056))
+    info = _append(ledger, a, 4096, list(range(256)) + [900])
     assert info["closed_page"] is None and info["new_history_pages"] == ()
-    with pytest.raises(ValueError, match="Skipped/replayed token"):
-        slots.append(a, 4096, list(range(256)) + [900])
-    with pytest.raises(ValueError, match="New physical page belongs to a live request"):
-        slots.append(b, 4096, list(range(256, 512)) + [900])
-    with pytest.raises(ValueError, match="Preemption/remapping"):
-        slots.append(b, 4096, list(range(257, 513)) + [901])
-    slots.release(a)
+    assert ledger.owner(900) == a
+    with pytest.raises(ValueError, match="skipped or replayed token"):
+        _append(ledger, a, 4096, list(range(256)) + [900])
+    with pytest.raises(ValueError, match="New physical page 900 belongs to a live request"):
+        _append(ledger, b, 4096, list(range(256, 512)) + [900])
+    with pytest.raises(ValueError, match="remapping"):
+        _append(ledger, b, 4096, list(range(257, 513)) + [901])
+    ledger.release(a)
+    assert ledger.owner(900) is None and ledger.owner(0) is None
     with pytest.raises(ValueError, match="Stale request lease"):
-        slots.state(a)
-    again = slots.admit("a", 4096, range(256))
+        ledger.view(a)
+    again = ledger.admit("a", 4096, range(256))
     assert (again.slot, again.generation) == (0, 2)        # the slot is reused, generation bumped
-    with pytest.raises(ValueError, match="Wrong/duplicate physical block table"):
-        slots.admit("d", 4096, [0] * 256)
+    with pytest.raises(ValueError, match="Wrong physical block table"):
+        ledger.admit("d", 4096, [0] * 256)
+    with pytest.raises(ValueError, match="Wrong physical block table"):
+        sv.Ledger(1, pool_pages=100).admit("e", 4096, range(256))   # ids beyond the pool
 
 
 def test_pages_age_into_history_only_when_complete():
-    slots = sv.RequestSlots(1, sv.Policy(prefix_pages=1, suffix_pages=2, tail_pages=2))
-    lease = slots.admit("a", 160, range(10))                # 10 pages; history 1..6
+    ledger = sv.Ledger(1, sv.Policy(prefix_pages=1, suffix_pages=2, tail_pages=2))
+    lease = ledger.admit("a", 160, range(10), ready=True)   # 10 pages; history 1..6
     table = list(range(10))
     aged = []
     for position in range(160, 160 + 40):
         if position % 16 == 0:
             table.append(100 + position // 16)
-        info = slots.append(lease, position, table)
+        info = _append(ledger, lease, position, table)
         aged.extend(info["new_history_pages"])
         for page in info["new_history_pages"]:
             assert page < (position + 1) // 16             # only completed pages
@@ -110,47 +120,98 @@ def test_pages_age_into_history_only_when_complete():
     assert aged == [10]
 
 
-def test_prepare_and_commit_decode_match_the_reference_bridge():
-    slots = sv.RequestSlots(2)
-    a = slots.admit("a", 4096, range(256))
-    batch = sv.prepare_decode(slots, [(a, 4096, list(range(256)) + [512])])
-    row = batch.rows[0]
-    assert row.physical_token_slot == 512 * 16                 # test_pinned_scheduler_bridge.py:66
+def test_staged_decode_steps_match_the_reference_bridge():
+    ledger = sv.Ledger(3)
+    a = ledger.admit("a", 4096, range(256), ready=True)
+    step = ledger.stage_decode([(a, 4096, list(range(256)) + [512])])
+    row = step.rows[0]
+    assert row.physical_token_slot == 512 * 16                 # test_pinned_scheduler_bridge.py:61
     assert row.exact_token_slot == sv.exact_slot(256, 4096, a.slot) * 16
-    assert batch.columns()["positions"] == (4096,)
-    assert slots.state(a).current_tokens == 4096               # non-mutating
-    sv.commit_decode(slots, batch)
-    assert slots.state(a).current_tokens == 4097
-    with pytest.raises(ValueError, match="Decode batch is stale"):
-        sv.commit_decode(slots, batch)
+    assert step.columns()["positions"] == (4096,)
+    assert ledger.view(a).current_tokens == 4096               # staging changes nothing
+    assert ledger.owner(512) is None
+    ledger.commit_decode(step)
+    assert ledger.view(a).current_tokens == 4097 and ledger.owner(512) == a
+    with pytest.raises(ValueError, match="Decode step is stale"):
+        ledger.commit_decode(step)
     with pytest.raises(ValueError, match="Wrong next token position"):
-        sv.prepare_decode(slots, [(a, 4096, list(range(256)) + [512])])
-    b = slots.admit("b", 4096, range(600, 856))
-    with pytest.raises(ValueError, match="Physical page alias across batch"):
-        sv.prepare_decode(slots, [(a, 4097, list(range(256)) + [512]),
-                                  (b, 4096, list(range(600, 856)) + [512])])
+        ledger.stage_decode([(a, 4096, list(range(256)) + [512])])
+    b = ledger.admit("b", 4096, range(600, 856), ready=True)
+    c = ledger.admit("c", 4096, range(900, 1156), ready=True)
+    with pytest.raises(ValueError, match="aliased across the step"):
+        ledger.stage_decode([(b, 4096, list(range(600, 856)) + [513]),
+                             (c, 4096, list(range(900, 1156)) + [513])])
     with pytest.raises(ValueError, match="Duplicate scheduled request"):
-        sv.prepare_decode(slots, [(b, 4096, list(range(600, 856)) + [900])] * 2)
+        ledger.stage_decode([(b, 4096, list(range(600, 856)) + [2000])] * 2)
+    # a page claimed after staging makes the staged step stale
+    step_b = ledger.stage_decode([(b, 4096, list(range(600, 856)) + [3000])])
+    ledger.commit_decode(ledger.stage_decode([(c, 4096, list(range(900, 1156)) + [3000])]))
+    with pytest.raises(ValueError, match="claimed after staging"):
+        ledger.commit_decode(step_b)
+    assert ledger.view(b).current_tokens == 4096
+
+
+def test_slot_phases():
+    class Event:
+        def __init__(self, done):
+            self.done = done
+
+        def query(self):
+            return self.done
+
+    ledger = sv.Ledger(2, num_layers=3)
+    lease = ledger.admit("a", 4096, range(256))
+    assert ledger.phase(lease) is sv.Phase.PREFILL
+    with pytest.raises(RuntimeError, match="not decodable"):
+        ledger.stage_decode([(lease, 4096, list(range(256)) + [300])])
+    with pytest.raises(ValueError, match="completion event"):
+        ledger.mark_packed(lease, [0, 1, 2], object())
+    with pytest.raises(ValueError, match="Every layer must be packed exactly once"):
+        ledger.mark_packed(lease, [0, 1], Event(True))
+    event = Event(False)
+    ledger.mark_packed(lease, [2, 0, 1], event)
+    with pytest.raises(ValueError, match="Packing already submitted"):
+        ledger.mark_packed(lease, [0, 1, 2], event)
+    assert not ledger.is_ready(lease) and ledger.phase(lease) is sv.Phase.PACKING
+    event.done = True
+    assert ledger.is_ready(lease)
+    step = ledger.stage_decode([(lease, 4096, list(range(256)) + [300])])
+    assert ledger.commit_decode(step)[0]["position"] == 4096
+    with pytest.raises(ValueError, match="retire"):
+        ledger.reclaim(lease)
+    last = Event(False)
+    ledger.retire(lease, last)
+    with pytest.raises(ValueError, match="already retiring"):
+        ledger.retire(lease, last)
+    with pytest.raises(RuntimeError, match="not decodable"):
+        ledger.stage_decode([(lease, 4097, list(range(256)) + [300])])
+    assert not ledger.reclaim(lease)
+    last.done = True
+    assert ledger.reclaim(lease) and ledger.owner(300) is None
+    with pytest.raises(ValueError, match="Stale request lease"):
+        ledger.is_ready(lease)
+    with pytest.raises(ValueError, match="Positive layer count"):
+        sv.Ledger(1, num_layers=0)
 
 
 def test_decode_tables_cover_the_context_once():
     pol = sv.Policy(prefix_pages=2, suffix_pages=4, tail_pages=6)
-    slots = sv.RequestSlots(3, pol)
+    ledger = sv.Ledger(3, pol)
     leases, tables = [], []
     for name, prompt, base in (("a", 800, 0), ("b", 1000, 100), ("c", 1200, 200)):
         pages = list(range(base, base + (prompt + 15) // 16))
-        leases.append(slots.admit(name, prompt, pages))
+        leases.append(ledger.admit(name, prompt, pages, ready=True))
         tables.append(pages)
     scheduled = []
     for lease, table in zip(leases, tables):
-        position = slots.state(lease).current_tokens
+        position = ledger.view(lease).current_tokens
         if position % 16 == 0:
             table = table + [1000 + len(table) + 100 * lease.slot]
         scheduled.append((lease, position, table))
-    batch = sv.prepare_decode(slots, scheduled)
-    t = sv.decode_tables(batch, pol, device="cpu")
+    step = ledger.stage_decode(scheduled)
+    t = sv.decode_tables(step, pol, device="cpu")
     for r, (lease, position, table) in enumerate(scheduled):
-        prompt = slots.state(lease).prompt_tokens
+        prompt = ledger.view(lease).prompt_tokens
         part = sv.partition(prompt, position + 1, pol)
         old = t.old_indices[t.old_indptr[r]:t.old_indptr[r + 1]].tolist()
         exact = t.exact_indices[t.exact_indptr[r]:t.exact_indptr[r + 1]].tolist()
@@ -182,5 +243,5 @@ def test_dense_pool_views_split_one_allocation():
     assert views["key_codes"].shape == (4, 16, 8, 128) and views["value_scales"].shape == (4, 8)
     views["value_scales"].fill_(1.0)
     assert raw[-2:].view(torch.float16).item() == 1.0
-    with pytest.raises(ValueError, match="exact size"):
+    with pytest.raises(ValueError, match="exactly"):
         sv.dense_pool_views(raw[:-2], 4, 8)

@@ -15,8 +15,7 @@ import pytest
 import torch
 
 from pagegauge_amd import serving as sv
-from pagegauge_amd.serving_bridge import (UNSUPPORTED_FIELDS, PendingDeviceWork,
-                                          PrefillLifecycle, SchedulerBridge)
+from pagegauge_amd.serving_bridge import UNSUPPORTED_FIELDS, PendingDeviceWork, SchedulerBridge
 
 
 class Event:
@@ -78,12 +77,14 @@ def test_mixed_prefill_and_decode_wait_for_every_layer_and_the_event(bridge):
     assert bridge.state("a").current_tokens == 4096
     with pytest.raises(RuntimeError, match="still in flight"):
         bridge.apply(message())
+    assert bridge.ledger.phase(step.prefills[0].lease) is sv.Phase.PREFILL
     event.done = True
     with pytest.raises(ValueError, match="Every layer must be packed exactly once"):
         bridge.complete(step, {step.prefills[0].lease: [0]}, event)
     assert bridge.state("a").current_tokens == 4096
     assert bridge.complete(step, layers, event)
     assert bridge.state("a").current_tokens == 4097 and bridge.state("b").current_tokens == 4096
+    assert bridge.ledger.phase(bridge.state("b").lease) is sv.Phase.READY
     with pytest.raises(ValueError, match="stale or already completed"):
         bridge.complete(step, layers, event)
 
@@ -187,42 +188,6 @@ def test_abort_reclaims_only_the_scheduled_leases_after_the_fence(bridge):
     assert bridge.state("b").lease == b
 
 
-def test_lifecycle_phases():
-    life = PrefillLifecycle(2, 3)
-    lease = life.begin("a", 4096, (list(range(256)),))
-    with pytest.raises(RuntimeError, match="before packing completion"):
-        life.decode_batch(["a"])
-    with pytest.raises(ValueError, match="A recorded completion event is required"):
-        life.submit_packing(lease, [0, 1, 2], object())
-    event = Event(False)
-    life.submit_packing(lease, [2, 0, 1], event)
-    with pytest.raises(ValueError, match="Packing already submitted"):
-        life.submit_packing(lease, [0, 1, 2], event)
-    assert not life.ready(lease)
-    event.done = True
-    assert life.ready(lease) and life.decode_batch(["a"])[0].lease == lease
-    batch = life.prepare_decode([(lease, 4096, list(range(256)) + [300])])
-    pending = Event(False)
-    assert life.commit_decode(batch, pending) is None
-    pending.done = True
-    assert life.commit_decode(batch, pending)[0]["position"] == 4096
-    with pytest.raises(ValueError, match="Explicit finish/abort event required"):
-        life.reclaim(lease)
-    last = Event(False)
-    life.retire(lease, last)
-    with pytest.raises(ValueError, match="Lease already retiring"):
-        life.retire(lease, last)
-    assert not life.reclaim(lease)
-    last.done = True
-    assert life.reclaim(lease)
-    with pytest.raises(ValueError, match="Stale request lease"):
-        life.ready(lease)
-    with pytest.raises(ValueError, match="Prefix reuse/chunked prefill"):
-        life.begin("b", 4096, (list(range(256)),), num_computed_tokens=16)
-    with pytest.raises(ValueError, match="Positive layer count"):
-        PrefillLifecycle(1, 0)
-
-
 def test_bridge_never_initialises_the_gpu():
     assert not torch.cuda.is_initialized()
 
@@ -255,7 +220,7 @@ def test_engine_layer_views_keep_their_offset_and_zeroing_keeps_other_pages():
     for t in views.values():
         t.fill_(1)
     assert not backing[0].any() and backing[1].any()
-    with pytest.raises(ValueError, match="Compact packed engine layer"):
+    with pytest.raises(ValueError, match="compact packed engine layer"):
         sv.from_engine_layer(torch.zeros((3, 2, 8, 1, 4100), dtype=torch.uint8)[:, 0], 3, 8)
     raw = torch.empty(4 * 32800, dtype=torch.uint8)
     views = sv.dense_pool_views(raw, 4, 8)
