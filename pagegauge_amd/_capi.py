@@ -114,6 +114,8 @@ PROTOTYPES = {
     "pg_merge_state_in_place": (_i32, [_p, _p, _p, _p, _p, _i32, _i32, _i32, _p]),
     "pg_exact_tail_merge_center": (_i32, [_p, _p, _p, _p, _p, _p, _p, _p, _i64, _i32, _i32, _i32,
                                           _i32, _f32, _p]),
+    "pg_probe_linear_read": (_i32, [_p, _i64, _p, _i32, _p, _p, _p]),
+    "pg_probe_page_walk": (_i32, [_p, _p, _p, _i32, _i32, _i32, _p, _p, _p, _p]),
 }
 
 _lock = threading.Lock()

@@ -38,6 +38,7 @@ SOURCES = {
     "pg_update.hip": ["-ffp-contract=off"],
     "pg_decode.hip": [],
     "pg_decoder.hip": [],
+    "pg_probe.hip": [],
 }
 
 

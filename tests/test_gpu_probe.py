@@ -1,0 +1,37 @@
+"""The HBM read probes (measurement helpers of bench.py's roofline peak):
+they launch, leave the sink untouched for data that cannot hit the sink's
+condition, time themselves through dispatch-stamped events, and reject bad
+arguments."""
+
+from __future__ import annotations
+
+import pytest
+import torch
+
+from pagegauge_amd import _capi
+
+pytestmark = pytest.mark.gpu
+
+
+def test_probes_read_and_time_themselves(cuda):
+    lib = _capi.library()
+    stream = torch.cuda.current_stream().cuda_stream
+    data = torch.zeros(1 << 20, dtype=torch.int32, device=cuda)
+    sink = torch.full((4096,), 7, dtype=torch.int32, device=cuda)
+    start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record()
+    stop.record()
+    torch.cuda.synchronize()
+    assert lib.pg_probe_linear_read(data.data_ptr(), data.numel() * 4, sink.data_ptr(), 512,
+                                    start.cuda_event, stop.cuda_event, stream) == 0
+    pages = torch.zeros(8, 16, 8, 128, dtype=torch.int8, device=cuda)
+    ids = torch.tensor([5, 0, 7, 2], dtype=torch.int32, device=cuda)
+    assert lib.pg_probe_page_walk(pages.data_ptr(), pages.data_ptr(), ids.data_ptr(), 4, 2, 16384,
+                                  sink.data_ptr(), None, None, stream) == 0
+    torch.cuda.synchronize()
+    assert start.elapsed_time(stop) > 0.0
+    assert bool((sink == 7).all())             # zero data never meets the write condition
+    assert lib.pg_probe_linear_read(data.data_ptr(), 17, sink.data_ptr(), 1, None, None, stream) == 1
+    assert "16-byte" in _capi.last_error()
+    assert lib.pg_probe_page_walk(None, None, None, 1, 1, 16, sink.data_ptr(), None, None,
+                                  stream) == 1

@@ -650,3 +650,135 @@ def test_heterogeneous_oracle_is_dense_softmax_over_logical_sequence(old_tokens,
             want = p @ logical_v[r][:, g] + center[r, g].astype(np.float64)
             assert np.abs(got[r, h] - want).max() < 1e-9
     assert np.isfinite(got).all() and np.isfinite(lse).all()
+
+
+# ---------------------------------------------------------------------------
+# The torch-CPU restatement timed as the CPU baseline (oracle/cpu_baseline.py)
+# ---------------------------------------------------------------------------
+
+def _ragged_int8_case(seed=3):
+    rng = np.random.default_rng(seed)
+    lengths = [3, 1, 0]                      # history pages per request (one empty)
+    tails = [2, 1, 1]
+    pool = sum(lengths) + 2
+    k = rng.integers(-127, 128, (pool, 16, 2, 128), dtype=np.int8)
+    v = rng.integers(-127, 128, (pool, 16, 2, 128), dtype=np.int8)
+    ks = (rng.random((pool, 2)) * 1e-2 + 1e-3).astype(np.float16)
+    vs = (rng.random((pool, 2)) * 1e-2 + 1e-3).astype(np.float16)
+    perm = rng.permutation(pool)[:sum(lengths)].astype(np.int32)
+    indptr = np.cumsum([0] + lengths).astype(np.int32)
+    ring = sum(tails) + 1
+    tk = (rng.standard_normal((ring, 16, 2, 128)) * 0.3).astype(np.float16)
+    tv = (rng.standard_normal((ring, 16, 2, 128)) * 0.3).astype(np.float16)
+    tail_indptr = np.cumsum([0] + tails).astype(np.int32)
+    tail_indices = rng.permutation(ring)[:sum(tails)].astype(np.int32)
+    q = (rng.standard_normal((3, 8, 128)) * 0.5).astype(np.float16)
+    center = (rng.standard_normal((3, 2, 128)) * 0.05).astype(np.float16)
+    return dict(query=q, k_pages=k, v_pages=v, indptr=indptr, indices=perm,
+                last_page_len=np.array([16, 16, 16], np.int32), sm_scale=128 ** -0.5,
+                k_scale=ks, v_scale=vs, tail_k=tk, tail_v=tv, tail_indptr=tail_indptr,
+                tail_indices=tail_indices, tail_last_page_len=np.array([5, 16, 1], np.int32),
+                value_center=center)
+
+
+def test_cpu_baseline_decode_matches_the_oracle():
+    import torch
+
+    from oracle import cpu_baseline as cb
+
+    case = _ragged_int8_case()
+    want_out, want_lse, _ = oracle.decode(**case)
+    as_torch = {k: (torch.from_numpy(v) if isinstance(v, np.ndarray) else v) for k, v in case.items()}
+    out, lse = cb.decode_dense(**as_torch)
+    assert np.abs(out.numpy().astype(np.float64) - want_out.astype(np.float64)).max() <= 1e-3
+    assert np.abs(lse.numpy().astype(np.float64) - want_lse.astype(np.float64)).max() <= 1e-4
+    # a plausible mistake (GQA heads regrouped as head-major g*Hkv + kv) is caught
+    bad = dict(as_torch, query=as_torch["query"].view(3, 4, 2, 128).transpose(1, 2).reshape(3, 8, 128))
+    out_bad, _ = cb.decode_dense(**bad)
+    assert np.abs(out_bad.numpy().astype(np.float64) - want_out.astype(np.float64)).max() > 1e-2
+
+
+def test_cpu_baseline_append_is_bit_exact_with_the_oracle():
+    import torch
+
+    from oracle import cpu_baseline as cb
+
+    rng = np.random.default_rng(11)
+    batch, hkv, ring, code_pages, sink = 3, 2, 3, 6, 1
+    cos_np, sin_np = oracle.rope_tables(code_pages * 16)
+    kc = (rng.standard_normal((batch, hkv, 128)) * 0.1).astype(np.float16)
+    vc = (rng.standard_normal((batch, hkv, 128)) * 0.1).astype(np.float16)
+    shapes = [(batch * ring, 16, hkv, 128)] * 2
+    host = [np.zeros(s, np.float16) for s in shapes]
+    host += [np.zeros((batch * code_pages, 16, hkv, 128), np.int8) for _ in range(2)]
+    host += [np.zeros((batch * code_pages, hkv), np.float16) for _ in range(2)]
+    mine = [torch.from_numpy(a.copy()) for a in host]
+    rq_host = np.zeros((batch, 8, 128), np.float16)
+    rq = torch.zeros(batch, 8, 128, dtype=torch.float16)
+    start = np.array([0, 5, 17], np.int32)
+    for step in range(40):
+        q = (rng.standard_normal((batch, 8, 128))).astype(np.float16)
+        k = (rng.standard_normal((batch, hkv, 128))).astype(np.float16)
+        v = (rng.standard_normal((batch, hkv, 128))).astype(np.float16)
+        pos = start + step
+        oracle.rope_append_page_gauge_positions(q, k, v, cos_np, sin_np, pos, kc, vc, rq_host,
+                                                *host, sink)
+        cb.append_positions(torch.from_numpy(q), torch.from_numpy(k), torch.from_numpy(v),
+                            torch.from_numpy(cos_np), torch.from_numpy(sin_np),
+                            torch.from_numpy(pos), torch.from_numpy(kc), torch.from_numpy(vc), rq,
+                            *mine, sink)
+        assert np.array_equal(rq.numpy().view(np.uint16), rq_host.view(np.uint16)), step
+    for got, want in zip(mine, host):
+        assert np.array_equal(got.numpy().view(np.uint8), want.view(np.uint8))
+    assert np.abs(host[5]).max() > 0                      # pages were finalized
+
+
+def test_cpu_baseline_decoder_step_matches_transformers():
+    """One step of the CPU decoder against MistralForCausalLM with the same
+    weights, its KV cache holding the reconstruction of the PageGauge cache
+    (K = c + s*Z or c + ring) and the new token at the next position."""
+    import torch
+    from transformers import DynamicCache, MistralConfig, MistralForCausalLM
+
+    from oracle import cpu_baseline as cb
+
+    layers, context, hidden, qh, kvh, inter, vocab = 2, 160, 512, 4, 1, 256, 64
+    d = cb.CpuDecoder(layers, context, 9, hidden=hidden, q_heads=qh, kv_heads=kvh,
+                      intermediate=inter, vocab=vocab, tail_pages=3, steps=4, std=0.05)
+    hf = MistralForCausalLM(MistralConfig(
+        vocab_size=vocab, hidden_size=hidden, intermediate_size=inter, num_hidden_layers=layers,
+        num_attention_heads=qh, num_key_value_heads=kvh, head_dim=128, rope_theta=1.0e6,
+        rms_norm_eps=1e-5, max_position_embeddings=512, tie_word_embeddings=False,
+        attn_implementation="eager"))
+    qw, kw = qh * 128, kvh * 128
+    cache = DynamicCache()
+    with torch.no_grad():
+        hf.model.embed_tokens.weight.copy_(d.embed)
+        hf.lm_head.weight.copy_(d.lm_head)
+        for i, (layer, w, c) in enumerate(zip(hf.model.layers, d.layers, d.cache)):
+            layer.self_attn.q_proj.weight.copy_(w["qkv"][:qw])
+            layer.self_attn.k_proj.weight.copy_(w["qkv"][qw:qw + kw])
+            layer.self_attn.v_proj.weight.copy_(w["qkv"][qw + kw:])
+            layer.self_attn.o_proj.weight.copy_(w["o"])
+            layer.mlp.gate_proj.weight.copy_(w["gate_up"][:inter])
+            layer.mlp.up_proj.weight.copy_(w["gate_up"][inter:])
+            layer.mlp.down_proj.weight.copy_(w["down"])
+            pages = context // 16
+            old = pages - d.tail_pages
+            keys = torch.cat((c["codes_k"][:old].float() * c["scales_k"][:old].float()[:, None, :, None],
+                              c["exact_k"][[p % d.tail_pages for p in range(old, pages)]].float()))
+            vals = torch.cat((c["codes_v"][:old].float() * c["scales_v"][:old].float()[:, None, :, None],
+                              c["exact_v"][[p % d.tail_pages for p in range(old, pages)]].float()))
+            keys = keys.reshape(context, kvh, 128) + c["key_center"].float()
+            vals = vals.reshape(context, kvh, 128) + c["value_center"].float()
+            cache.update(keys.permute(1, 0, 2)[None].contiguous(),
+                         vals.permute(1, 0, 2)[None].contiguous(), i)
+    hf.eval()
+    token = 17
+    with torch.no_grad():
+        want = hf(torch.tensor([[token]]), position_ids=torch.tensor([[context]]),
+                  past_key_values=cache, use_cache=True).logits[0, -1]
+    got = d.step(token, context)
+    scale = float(want.abs().max())
+    print("cpu decoder step vs transformers", float((got - want).abs().max()), scale)
+    assert float((got - want).abs().max()) <= 2e-2 * scale
