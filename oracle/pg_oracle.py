@@ -47,8 +47,11 @@ PINNED = {
     "quantize_page_gauge": "torch transcription of scripts/benchmark_flashinfer_page_affine_int8.py:256-278",
     "quantize_completed_kv_pages": "torch transcription of scripts/benchmark_page_gauge_overheads.py:23-83",
     "append_finalize_page_gauge": "equivalence with rope_append_page_gauge at identity RoPE",
+    "append_kv": "the reference's cross-check of its two appends "
+    "(scripts/benchmark_page_gauge_overheads.py:556-609: fused exact pages + center within "
+    "2e-3 of the plain pages, codes reconstruct them < 0.03) and direct placement",
     "rope_append_page_gauge_slots": "equivalence with rope_append_page_gauge_positions when the "
-    "ids are the request-major slots",
+    "ids are the request-major slots (tests/test_oracle.py, CPU), skipped rows for bad ids",
     "decode": "torch float64 softmax attention; logsumexp identity; merge associativity",
     "merge_state": "decode(A u B) == merge(decode(A), decode(B))",
     "exact_tail_merge_center": "torch oracle of tests/test_page_gauge_append_extension.py:628-657",

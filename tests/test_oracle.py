@@ -356,6 +356,115 @@ def test_positions_variant_equals_scalar_kernel_row_by_row():
             assert _bits_equal(a[name][rows], b[name][rows]), name
 
 
+def test_slots_variant_equals_positions_variant_on_request_major_ids():
+    """rope_append_page_gauge_slots with the request-major ids that the
+    positions variant derives (exact page r*E + ring slot of the position's
+    page, code page r*P + page) writes exactly what the positions variant
+    writes, over 40 steps with ring wraps and finalizes; a row whose id is
+    negative or outside the pool is skipped."""
+    batch, ring, code_pages, sink = 3, 3, 6, 1
+    cos_t, sin_t = oracle.rope_tables(code_pages * 16)
+    kc, vc = _f16((batch, 8, 128), 0.1), _f16((batch, 8, 128), 0.1)
+    a = _fresh_page_gauge_buffers(batch, ring, code_pages)
+    b = _fresh_page_gauge_buffers(batch, ring, code_pages)
+    start = np.array([0, 7, 30], np.int32)
+    for step in range(40):
+        query, key, value = _f16((batch, 32, 128)), _f16((batch, 8, 128)), _f16((batch, 8, 128))
+        pos = start + step
+        pages = pos // 16
+        local = np.where(pages < sink, pages, sink + pages % (ring - sink))
+        exact_ids = np.arange(batch) * ring + local
+        code_ids = np.arange(batch) * code_pages + pages
+        oracle.rope_append_page_gauge_positions(query, key, value, cos_t, sin_t, pos, kc, vc,
+                                                exact_sink_pages=sink, **a)
+        oracle.rope_append_page_gauge_slots(query, key, value, cos_t, sin_t, pos, exact_ids,
+                                            code_ids, kc, vc, **b)
+    for name in a:
+        assert _bits_equal(a[name], b[name]), name
+    assert np.abs(a["key_scales"]).max() > 0
+    before = {k: v.copy() for k, v in b.items()}
+    oracle.rope_append_page_gauge_slots(query, key, value, cos_t, sin_t, pos,
+                                        np.array([-1, batch * ring, 0]), np.array([0, 0, -1]),
+                                        kc, vc, **b)
+    for name in b:
+        if name != "rotated_query":
+            assert _bits_equal(b[name], before[name]), name
+
+
+def test_append_kv_against_the_fused_append_relation():
+    """The reference's own cross-check of its two appends
+    (scripts/benchmark_page_gauge_overheads.py:556-609): after one 16-step
+    cycle at offsets 0..15, the fused append's exact pages plus the center
+    equal the plain append's pages within 2e-3 (one FP16 rounding of the
+    centered value), and its codes reconstruct them with relative L2 < 0.03.
+    The plain append is also the FP16 append at identity RoPE placed at
+    (page_ids, offsets)."""
+    batch, heads = 3, 2
+    page_ids = np.array([4, 0, 2], np.int32)
+    kc, vc = _f16((heads, 128), 0.1), _f16((heads, 128), 0.1)
+    plain = [np.zeros((6, 16, heads, 128), np.float16) for _ in range(2)]
+    fused = [np.zeros((6, 16, heads, 128), np.float16) for _ in range(2)]
+    fused += [np.zeros((6, 16, heads, 128), np.int8) for _ in range(2)]
+    fused += [np.zeros((6, heads), np.float16) for _ in range(2)]
+    keys = [_f16((batch, heads, 128)) for _ in range(16)]
+    values = [_f16((batch, heads, 128)) for _ in range(16)]
+    for t in range(16):
+        offsets = np.full(batch, t, np.int32)
+        oracle.append_kv(keys[t], values[t], *plain, page_ids, offsets)
+        oracle.append_finalize_page_gauge(keys[t], values[t], kc, vc, *fused, page_ids, offsets)
+    for r, page in enumerate(page_ids):
+        for t in range(16):
+            assert _bits_equal(plain[0][page, t], keys[t][r])
+            assert _bits_equal(plain[1][page, t], values[t][r])
+    exact = fused[0][page_ids].astype(np.float32) + kc.astype(np.float32)
+    assert np.abs(exact - plain[0][page_ids].astype(np.float32)).max() <= 2e-3
+    recon = (fused[2][page_ids].astype(np.float32) * fused[4][page_ids].astype(np.float32)[:, None, :, None]
+             + kc.astype(np.float32))
+    base = plain[0][page_ids].astype(np.float32)
+    assert np.linalg.norm(recon - base) / np.linalg.norm(base) < 0.03
+    untouched = [p for p in range(6) if p not in page_ids]
+    assert not plain[0][untouched].any()
+
+
+@pytest.mark.parametrize("seed", range(6))
+def test_decode_fuzzed_page_tables(seed):
+    """Random ragged tables over one shared, shuffled pool (empty requests,
+    single pages, partial last pages, shared physical pages): the oracle's
+    paged decode equals the dense softmax over the tokens gathered page by
+    page in table order, and is invariant to renumbering the pool."""
+    rng = np.random.default_rng(1000 + seed)
+    batch = int(rng.integers(1, 5))
+    pool = int(rng.integers(2, 12))
+    k, v, ks, vs = _random_paged(pool, seed)
+    counts = rng.integers(0, 5, batch)
+    indptr = np.concatenate(([0], np.cumsum(counts))).astype(np.int32)
+    indices = rng.integers(0, pool, int(indptr[-1])).astype(np.int32)   # pages may repeat
+    last = rng.integers(1, 17, batch).astype(np.int32)
+    q = _f16((batch, 32, 128), 0.4)
+    out, lse, out64 = oracle.decode(q, k, v, indptr, indices, last, 128 ** -0.5, k_scale=ks,
+                                    v_scale=vs)
+    for r in range(batch):
+        ids = indices[indptr[r]:indptr[r + 1]]
+        if ids.size == 0:
+            assert np.isneginf(lse[r]).all() and not out64[r].any()
+            continue
+        keys = (k[ids].astype(np.float64) * ks[ids].astype(np.float64)[:, None, :, None])
+        vals = (v[ids].astype(np.float64) * vs[ids].astype(np.float64)[:, None, :, None])
+        n = (ids.size - 1) * 16 + int(last[r])
+        keys = keys.reshape(-1, 8, 128)[:n]
+        vals = vals.reshape(-1, 8, 128)[:n]
+        for h in range(32):
+            s = keys[:, h // 4] @ q[r, h].astype(np.float64) * 128 ** -0.5
+            p = np.exp(s - s.max())
+            assert np.allclose(out64[r, h], p @ vals[:, h // 4] / p.sum(), atol=1e-9)
+            assert abs(lse[r, h] - (np.log(p.sum()) + s.max()) / np.log(2)) < 1e-4
+    perm = rng.permutation(pool)
+    inverse = np.argsort(perm)
+    out2, _, _ = oracle.decode(q, k[perm], v[perm], indptr, inverse[indices].astype(np.int32), last,
+                               128 ** -0.5, k_scale=ks[perm], v_scale=vs[perm])
+    assert _bits_equal(out, out2)
+
+
 def test_rope_append_fp16_request_major_placement():
     """Identity RoPE + page request*P + position//16 (tests/test_page_gauge_append_extension.py:766-786)."""
     batch, pages = 3, 3
