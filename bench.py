@@ -76,6 +76,8 @@ def parse_args() -> argparse.Namespace:
     p.add_argument("--pilot", action="store_true",
                    help="the reference's split pilot sweep (B1/49K, B8 ragged x3, B1 16K, B1 64K): "
                         "prints one JSON line and exits")
+    p.add_argument("--workload", choices=("b1_49k", "config1"), default="b1_49k",
+                   help="workload of the --pmc-calls driver (config1: B=1, 4096 tokens)")
     p.add_argument("--pmc-calls", type=int, default=0,
                    help="counter-collection driver for rocprofv3 --pmc: N cold decode calls, "
                         "then N plain 64 MiB copies of known size; prints one JSON line, no timing")
@@ -907,7 +909,10 @@ def main() -> int:
                                       lambda: torch.amax(buf, dim=0, out=sink), 60)), flush=True)
         return 0
     t_setup = time.perf_counter()
-    w = workloads.b1_49k(args.seed, device=device, with_fp16_copy=not args.no_fp16)
+    if args.pmc_calls and args.workload == "config1":
+        w = workloads.single_4k(args.seed, device=device, with_fp16_copy=not args.no_fp16)
+    else:
+        w = workloads.b1_49k(args.seed, device=device, with_fp16_copy=not args.no_fp16)
     torch.cuda.synchronize()
     setup_s = time.perf_counter() - t_setup
 
