@@ -33,6 +33,7 @@ sweep instead.  Prints one JSON line.
 from __future__ import annotations
 
 import argparse
+import hashlib
 import json
 import math
 import os
@@ -76,6 +77,9 @@ def parse_args() -> argparse.Namespace:
     p.add_argument("--pilot", action="store_true",
                    help="the reference's split pilot sweep (B1/49K, B8 ragged x3, B1 16K, B1 64K): "
                         "prints one JSON line and exits")
+    p.add_argument("--library-variant", default=None,
+                   help="time an alternative build (python -m pagegauge_amd.build --variant NAME) "
+                        "instead of the product library; the JSON line names it")
     p.add_argument("--workload", choices=("b1_49k", "config1"), default="b1_49k",
                    help="workload of the --pmc-calls driver (config1: B=1, 4096 tokens)")
     p.add_argument("--pmc-calls", type=int, default=0,
@@ -892,6 +896,9 @@ def main() -> int:
     import numpy as np
     import torch
 
+    if args.library_variant:
+        from pagegauge_amd import _capi, build
+        _capi.LIBRARY_PATH = build.variant_library(args.library_variant)
     from pagegauge_amd import decode, workloads
 
     if not torch.cuda.is_available():
@@ -934,7 +941,8 @@ def main() -> int:
     scrub_clean = lambda: torch.amax(scrub_clean_buf, dim=0, out=scrub_sink)  # noqa: E731
 
     if args.pmc_calls:
-        print(json.dumps(pmc_driver(torch, bound, args.pmc_calls, scrub_clean, device)), flush=True)
+        print(json.dumps({**pmc_driver(torch, bound, args.pmc_calls, scrub_clean, device),
+                          "library_variant": args.library_variant}), flush=True)
         return 0
     if args.pilot:
         print(json.dumps(pilot_sweep(torch, decode, workloads, device, scrub_clean)), flush=True)
@@ -1087,6 +1095,8 @@ def main() -> int:
         "fused_append_increment_b1": overhead,
         "validation_seeds_b1_49k": seeds,
         "parity_vs_oracle": parity,
+        "library_variant": args.library_variant,
+        "output_sha256": hashlib.sha256(gpu_out.tobytes() + gpu_lse.tobytes()).hexdigest(),
         "split_sweep": sweep or None,
         "other_configs": other,
         "wall_s_timed_region": round(wall_s, 3),

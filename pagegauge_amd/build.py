@@ -5,6 +5,14 @@ Every kernel source is compiled for gfx950 only, with packed-FP32 code
 generation disabled (``-packed-fp32-ops``).  The cache-update source is also
 compiled with ``-ffp-contract=off`` because its FP16/FP32 arithmetic must
 round operation by operation; the decode source keeps contraction enabled.
+
+Alternative builds for measured design comparisons (``python -m
+pagegauge_amd.build --variant NAME``) go to ``lib/variants/NAME/``; the
+product never loads them:
+
+* ``qk_valu``: the INT8 path's QK contraction on the VALU
+  (``v_dot4_i32_i8`` over the same query digits, K rows re-laid through LDS)
+  instead of the i8 MFMA; identical integer scores.
 """
 
 from __future__ import annotations
@@ -42,6 +50,15 @@ SOURCES = {
 }
 
 
+VARIANTS = {
+    "qk_valu": {"pg_decode.hip": ["-DPG_QK_VALU=1"]},
+}
+
+
+def variant_library(name: str) -> Path:
+    return PACKAGE / "lib" / "variants" / name / "libpagegauge_hip.so"
+
+
 def hipcc() -> str:
     path = shutil.which("hipcc") or "/opt/rocm/bin/hipcc"
     if not Path(path).exists():
@@ -49,9 +66,9 @@ def hipcc() -> str:
     return path
 
 
-def _compile(source: str, extra: list[str]) -> Path:
+def _compile(source: str, extra: list[str], build_dir: Path) -> Path:
     src = CSRC / source
-    obj = BUILD / (src.stem + ".o")
+    obj = build_dir / (src.stem + ".o")
     cmd = [hipcc(), *COMMON_FLAGS, *extra, "-c", str(src), "-o", str(obj)]
     if source.endswith(".cpp"):
         cmd = ["g++", "-O2", "-std=c++17", "-fPIC", "-Wall", f"-I{ROOT / 'include'}", "-c", str(src),
@@ -62,23 +79,35 @@ def _compile(source: str, extra: list[str]) -> Path:
     return obj
 
 
-def build(verbose: bool = False) -> Path:
-    """Compile every source and link the shared library; returns its path."""
-    BUILD.mkdir(parents=True, exist_ok=True)
-    LIBRARY.parent.mkdir(parents=True, exist_ok=True)
-    with ThreadPoolExecutor(max_workers=min(len(SOURCES), os.cpu_count() or 1)) as pool:
-        objects = list(pool.map(lambda item: _compile(*item), SOURCES.items()))
-    tmp = LIBRARY.with_suffix(".so.tmp")
+def build(verbose: bool = False, variant: str | None = None) -> Path:
+    """Compile every source and link the shared library; returns its path.
+
+    ``variant`` names an alternative build from ``VARIANTS``."""
+    build_dir, library, sources = BUILD, LIBRARY, dict(SOURCES)
+    if variant is not None:
+        if variant not in VARIANTS:
+            raise ValueError(f"unknown variant {variant!r}; known: {sorted(VARIANTS)}")
+        build_dir, library = BUILD / "variants" / variant, variant_library(variant)
+        for source, flags in VARIANTS[variant].items():
+            sources[source] = sources[source] + flags
+    build_dir.mkdir(parents=True, exist_ok=True)
+    library.parent.mkdir(parents=True, exist_ok=True)
+    with ThreadPoolExecutor(max_workers=min(len(sources), os.cpu_count() or 1)) as pool:
+        objects = list(pool.map(lambda item: _compile(item[0], item[1], build_dir), sources.items()))
+    tmp = library.with_suffix(".so.tmp")
     cmd = [hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", *map(str, objects), "-o", str(tmp)]
     result = subprocess.run(cmd, capture_output=True, text=True)
     if result.returncode != 0:
         raise RuntimeError(f"linking failed:\n{' '.join(cmd)}\n{result.stdout}\n{result.stderr}")
-    os.replace(tmp, LIBRARY)
+    os.replace(tmp, library)
     if verbose:
-        print(f"built {LIBRARY}")
-    return LIBRARY
+        print(f"built {library}")
+    return library
 
 
 if __name__ == "__main__":
-    build(verbose=True)
+    import argparse
+    parser = argparse.ArgumentParser(description=__doc__.splitlines()[0])
+    parser.add_argument("--variant", choices=sorted(VARIANTS), default=None)
+    build(verbose=True, variant=parser.parse_args().variant)
     sys.exit(0)

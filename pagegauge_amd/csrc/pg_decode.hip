@@ -56,7 +56,21 @@ constexpr int kGroupPages = 4;          // INT8 pages per PV MFMA (k = 64 tokens
 #define PG_MAX_WAVES_PER_BLOCK 8
 #endif
 constexpr int kMaxWavesPerBlock = PG_MAX_WAVES_PER_BLOCK;   // KV heads (waves) per workgroup
+// QK contraction unit of the INT8 path: 0 = i8 MFMA (the product), 1 = VALU
+// v_dot4_i32_i8 over the same query digits (an alternative build for the
+// MFMA-vs-VALU comparison; same integer results).
+#ifndef PG_QK_VALU
+#define PG_QK_VALU 0
+#endif
+#if PG_QK_VALU
+// P digits (1 KiB), query digit rows [4 heads][3 digits][128 B], and the
+// group's K rows [4 pages][16 tokens][144 B] (rows padded by 16 B).
+constexpr int kQDigitBytes = 4 * 3 * 128;
+constexpr int kKRowPitch = 144;
+constexpr int kLdsPerWave = 1024 + kQDigitBytes + kGroupPages * 16 * kKRowPitch;
+#else
 constexpr int kLdsPerWave = 1024;       // INT8 P digits: [4 pages][4 heads][4 digit rows][16 tokens]
+#endif
 constexpr int kCombineThreads = 256;
 constexpr int kMaxItemsPerRequest = 4096;
 constexpr int kMaxChunkPages = 64;      // pages per work item (one wave lane per page)
@@ -382,6 +396,16 @@ __device__ __forceinline__ void int8_chunk(const DecodeArgs& a, const WorkItem& 
   const float inv_p = ldexpf(1.0f, -p_exp);
   const float my_svu = ldexpf(my_sv, p_exp);       // sV * 2^p_exp of this lane's page slot
 
+#if PG_QK_VALU
+  // query digit rows for the VALU contraction: row 3h+c holds digit c of head h
+  uint8_t* q_lds = lds + 1024;
+  uint8_t* k_lds = lds + 1024 + kQDigitBytes;
+  if (a_digit < 3) {
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+      *reinterpret_cast<v4i*>(q_lds + (a_head * 3 + a_digit) * 128 + 16 * kg + 64 * j) = qd[j];
+  }
+#endif
   // zero the wave's digit buffer once: digit row 3 of every head stays zero
   *reinterpret_cast<uint4*>(lds + 16 * lane) = uint4{0u, 0u, 0u, 0u};
   wave_lds_fence();
@@ -416,11 +440,43 @@ __device__ __forceinline__ void int8_chunk(const DecodeArgs& a, const WorkItem& 
     // ---- QK: exact integer dot products
     float s[kGroupPages];
     float svu[kGroupPages];
+#if PG_QK_VALU
+    // the K rows go through LDS so that lane (head kg, token m16) sees the
+    // whole row of its token; 3 digit dots per page with v_dot4_i32_i8
+    int dots[kGroupPages][3];
 #pragma unroll
     for (int i = 0; i < kGroupPages; ++i) {
+      *reinterpret_cast<v4i*>(k_lds + (i * 16 + m16) * kKRowPitch + 16 * kg) = cur.k[i][0];
+      *reinterpret_cast<v4i*>(k_lds + (i * 16 + m16) * kKRowPitch + 64 + 16 * kg) = cur.k[i][1];
+#pragma unroll
+      for (int c = 0; c < 3; ++c) dots[i][c] = 0;
+    }
+    wave_lds_fence();
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      v4i qv[3];
+#pragma unroll
+      for (int c = 0; c < 3; ++c) qv[c] = *reinterpret_cast<const v4i*>(q_lds + (kg * 3 + c) * 128 + 16 * j);
+#pragma unroll
+      for (int i = 0; i < kGroupPages; ++i) {
+        const v4i kr = *reinterpret_cast<const v4i*>(k_lds + (i * 16 + m16) * kKRowPitch + 16 * j);
+#pragma unroll
+        for (int c = 0; c < 3; ++c)
+#pragma unroll
+          for (int w = 0; w < 4; ++w) dots[i][c] = __builtin_amdgcn_sdot4(qv[c][w], kr[w], dots[i][c], false);
+      }
+    }
+    wave_lds_fence();
+#endif
+#pragma unroll
+    for (int i = 0; i < kGroupPages; ++i) {
+#if PG_QK_VALU
+      const v4i acc = {dots[i][0], dots[i][1], dots[i][2], 0};
+#else
       v4i acc = {0, 0, 0, 0};
       acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(qd[0], cur.k[i][0], acc, 0, 0, 0);
       acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(qd[1], cur.k[i][1], acc, 0, 0, 0);
+#endif
       const int slot = g * kGroupPages + i;
       const int ls = min(slot, count - 1);
       const float sk = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, my_sk), ls));
