@@ -783,14 +783,6 @@ __device__ __forceinline__ void fma4(float4& acc, float w, const float4& v) {
   acc.w += w * v.w;
 }
 
-// Sum over the lanes of a wave that share lane % 8 (xor 8, 16, 32).
-__device__ __forceinline__ float column_sum(float v) {
-  v += __shfl_xor(v, 8, kWave);
-  v += __shfl_xor(v, 16, kWave);
-  v += __shfl_xor(v, 32, kWave);
-  return v;
-}
-
 // Shared memory of one combine unit (256 threads).
 struct CombineShared {
   float wave_max[kCombineThreads / kWave];
@@ -805,25 +797,25 @@ struct CombineShared {
 //
 // One memory round trip: the partial rows are loaded for the plan's largest
 // item count while the request's own count is loaded; rows past the count
-// are dropped by selects (they may hold anything).  Thread (r, c) = (tid / 8,
-// tid % 8) holds rows r, r + 32, ... of float4 column c; the row reductions
-// are shuffle trees plus one LDS exchange between the four waves.
+// are dropped by selects (they may hold anything).  The 16 lanes of a DPP row
+// hold 16 item rows of one float4 column, so the row reductions are DPP
+// rotations within the row plus one LDS exchange between the four waves.
 __device__ __forceinline__ void combine_unit(const CombineArgs& a, int row_head, int quarter,
                                              int tid, bool active, CombineShared& sh) {
   const int request = row_head / a.num_qo_heads;
   const int qh = row_head % a.num_qo_heads;
-  const int r = tid / kCombineCols;
-  const int c = tid % kCombineCols;
   const int wave = tid / kWave;
   const int lane = tid % kWave;
+  // wave w, DPP row q, lane i of the row: float4 column (w % 2) * 4 + q, item
+  // row i + 16 * (w / 2) (+ 32 k); a column's rows reduce within one DPP row
+  const int c = (wave & 1) * 4 + (lane >> 4);
+  const int r = (lane & 15) + 16 * (wave >> 1);
   const int dim = 32 * quarter + 4 * c;
   const int64_t base = static_cast<int64_t>(row_head) * a.max_items;
   const float* pm = a.partial_m + base;
   const float* pl = a.partial_l + base;
   const float* po = a.partial_o + base * kHeadDim + dim;
 
-  // the value center of the 8 output threads is loaded first: it is usually
-  // cold and would otherwise end the critical path
   float center4[4] = {0.0f, 0.0f, 0.0f, 0.0f};
   if (active && tid < kCombineCols && a.value_center != nullptr) {
     const uint16_t* cv = a.value_center + request * a.center_batch_stride + (qh / kGqa) * kHeadDim +
@@ -857,7 +849,7 @@ __device__ __forceinline__ void combine_unit(const CombineArgs& a, int row_head,
   }
   for (int j = r + kCombineInRegs * kCombineRows; j < count; j += kCombineRows)
     local_max = fmaxf(local_max, pm[j]);
-  local_max = wave_max(local_max);
+  local_max = row16_max(local_max);
   if (lane == 0) sh.wave_max[wave] = local_max;
   __syncthreads();
   float m = sh.wave_max[0];
@@ -869,7 +861,7 @@ __device__ __forceinline__ void combine_unit(const CombineArgs& a, int row_head,
 #pragma unroll
   for (int k = 0; k < kCombineInRegs; ++k) {
     const bool in = r + k * kCombineRows < count;
-    const float w = (in && mv[k] != kNegInf) ? exp2f(mv[k] - m) : 0.0f;
+    const float w = (in && mv[k] != kNegInf) ? __builtin_amdgcn_exp2f(mv[k] - m) : 0.0f;
     if (in) {
       fma4(acc, w, ov[k]);
       lsum += w * lv[k];
@@ -877,30 +869,24 @@ __device__ __forceinline__ void combine_unit(const CombineArgs& a, int row_head,
   }
   for (int j = r + kCombineInRegs * kCombineRows; j < count; j += kCombineRows) {
     const float mj = pm[j];
-    const float w = mj == kNegInf ? 0.0f : exp2f(mj - m);
+    const float w = mj == kNegInf ? 0.0f : __builtin_amdgcn_exp2f(mj - m);
     fma4(acc, w, *reinterpret_cast<const float4*>(po + static_cast<int64_t>(j) * kHeadDim));
     lsum += w * pl[j];
   }
-  acc.x = column_sum(acc.x);
-  acc.y = column_sum(acc.y);
-  acc.z = column_sum(acc.z);
-  acc.w = column_sum(acc.w);
-  lsum = column_sum(lsum);          // column 0 lanes: the wave's l (every row counted once)
-  if (lane < kCombineCols) sh.wave_acc[wave][lane] = acc;
+  acc.x = row16_sum(acc.x);
+  acc.y = row16_sum(acc.y);
+  acc.z = row16_sum(acc.z);
+  acc.w = row16_sum(acc.w);
+  lsum = row16_sum(lsum);
+  if ((lane & 15) == 0) sh.wave_acc[wave][lane >> 4] = acc;
   if (lane == 0) sh.wave_l[wave] = lsum;
   __syncthreads();
   if (active && tid < kCombineCols) {
-    float4 total = sh.wave_acc[0][tid];
-    float l = sh.wave_l[0];
-#pragma unroll
-    for (int w = 1; w < kCombineThreads / kWave; ++w) {
-      const float4 v = sh.wave_acc[w][tid];
-      total.x += v.x;
-      total.y += v.y;
-      total.z += v.z;
-      total.w += v.w;
-      l += sh.wave_l[w];
-    }
+    // column tid: waves tid / 4 (rows 0-15) and 2 + tid / 4 (rows 16-31), DPP row tid % 4
+    const float4 v0 = sh.wave_acc[tid >> 2][tid & 3];
+    const float4 v1 = sh.wave_acc[2 + (tid >> 2)][tid & 3];
+    const float4 total = make_float4(v0.x + v1.x, v0.y + v1.y, v0.z + v1.z, v0.w + v1.w);
+    const float l = sh.wave_l[0] + sh.wave_l[2];
     const bool empty = !(l > 0.0f);
     const float inv = empty ? 0.0f : 1.0f / l;
     const float o4[4] = {total.x * inv + center4[0], total.y * inv + center4[1],
