@@ -770,10 +770,14 @@ def _quantile(values, probability):
     position = (len(ordered) - 1) * probability
     lower = int(position)
     upper = min(lower + 1, len(ordered) - 1)
-    return ordered[lower] + (ordered[upper] - ordered[lower]) * (position - lower)
+    fraction = position - lower
+    return ordered[lower] * (1.0 - fraction) + ordered[upper] * fraction
 
 
-def bootstrap_median_ci(values, samples: int = 20000, seed: int = 20260815):
+BOOTSTRAP_SEED = 20260815
+
+
+def bootstrap_median_ci(values, samples: int = 20000, seed: int = BOOTSTRAP_SEED):
     """95 % bootstrap interval of the median over seeds (resampling with
     replacement; scripts/summarize_page_gauge_results.py:34-41)."""
     import random
@@ -822,12 +826,16 @@ def seed_study(torch, decode, workloads, device, seeds, scrub, overhead, repeats
     summary = {"seeds": list(seeds), "per_seed": per_seed,
                "append_increment_source": "append_overhead (B=1, paired, 16-step cycles)"}
     for mode in ("cache_neutral", "cache_hot"):
-        for key in ("attention_only_speedup", "inclusive_speedup"):
+        # the reference resamples the inclusive ratios with the next seed
+        # (scripts/summarize_page_gauge_results.py:56-69)
+        for key, seed_offset in (("attention_only_speedup", 0), ("inclusive_speedup", 1)):
             values = [r[mode][key] for r in per_seed]
             summary.setdefault(mode, {})[key] = {
                 "median": round(statistics.median(values), 4),
                 "range": [min(values), max(values)],
-                "seed_bootstrap_median_95_ci": bootstrap_median_ci(values) if len(values) > 1 else None}
+                "seed_bootstrap_median_95_ci": (
+                    bootstrap_median_ci(values, seed=BOOTSTRAP_SEED + seed_offset)
+                    if len(values) > 1 else None)}
         summary[mode]["int8_p50_us_median"] = round(
             statistics.median(r[mode]["int8_p50_us"] for r in per_seed), 3)
     return summary
