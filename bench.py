@@ -77,6 +77,10 @@ def parse_args() -> argparse.Namespace:
     p.add_argument("--pilot", action="store_true",
                    help="the reference's split pilot sweep (B1/49K, B8 ragged x3, B1 16K, B1 64K): "
                         "prints one JSON line and exits")
+    p.add_argument("--stream-probe", action="store_true",
+                   help="time load-only walks of the B1/49K pages in the decode kernel's own "
+                        "access pattern (pg_probe_decode_walk) beside the kernel; prints one "
+                        "JSON line and exits")
     p.add_argument("--library-variant", default=None,
                    help="time an alternative build (python -m pagegauge_amd.build --variant NAME) "
                         "instead of the product library; the JSON line names it")
@@ -844,6 +848,83 @@ def seed_study(torch, decode, workloads, device, seeds, scrub, overhead, repeats
     return summary
 
 
+# (label, table entries, pages per item, KV heads per workgroup, groups in
+# flight, lane pattern) of pg_probe_decode_walk.  3024 = 108 items of 28 pages
+# (the planner's B1/49K items), 3040 = 95 x 32 = 190 x 16 = 380 x 8.
+STREAM_PROBES = (
+    ("decode pattern, 28-page items, 4 heads per workgroup, 2 groups in flight", 3024, 28, 4, 2, 0),
+    ("decode pattern, 28-page items, 4 heads per workgroup, 1 group in flight", 3024, 28, 4, 1, 0),
+    ("decode pattern, 16-page items, 8 heads per workgroup", 3040, 16, 8, 2, 0),
+    ("decode pattern, 8-page items, 4 heads per workgroup", 3040, 8, 4, 2, 0),
+    ("whole head rows, 32-page items, 4 heads per workgroup", 3040, 32, 4, 2, 1),
+    ("whole head rows, 16-page items, 8 heads per workgroup", 3040, 16, 8, 2, 1),
+    ("whole pages per workgroup, 16-page items", 3040, 16, 8, 2, 2),
+    ("whole pages per workgroup, 8-page items", 3040, 8, 8, 2, 2),
+)
+
+
+def stream_probe(torch, w, bound, scrub, samples: int = 20):
+    """Load-only walks of the B1/49K INT8 pages (pg_probe_decode_walk) in the
+    decode kernel's access pattern and in more favourable ones, cold (after
+    the clean scrub) and hot, beside the decode's partial kernel timed the
+    same way in the same process: how close the kernel comes to the stream of
+    its own pattern.  Mean of dispatch-stamped durations."""
+    from pagegauge_amd import _capi
+
+    lib = _capi.library()
+    stream = torch.cuda.current_stream().cuda_stream
+    sink = torch.empty(4096, dtype=torch.int32, device=w.query.device)
+    events = [[torch.cuda.Event(enable_timing=True) for _ in range(2)] for _ in range(samples)]
+    for pair in events:
+        for e in pair:
+            e.record()
+    torch.cuda.synchronize()
+
+    def timed(fn, before):
+        for _ in range(2):
+            if before is not None:
+                before()
+            fn(None, None)
+        for a, b in events:
+            if before is not None:
+                before()
+            fn(a.cuda_event, b.cuda_event)
+        torch.cuda.synchronize()
+        return 1e3 * statistics.fmean(a.elapsed_time(b) for a, b in events)
+
+    rows = []
+    for label, pages, per_item, heads, depth, mode in STREAM_PROBES:
+        def walk(start, stop, pages=pages, per_item=per_item, heads=heads, depth=depth, mode=mode):
+            _capi.check(lib.pg_probe_decode_walk(
+                w.k_codes.data_ptr(), w.v_codes.data_ptr(), w.old_indices.data_ptr(), pages,
+                per_item, heads, depth, mode, sink.data_ptr(), start, stop, stream), "probe")
+        cold, hot = timed(walk, scrub), timed(walk, None)
+        nbytes = pages * 2 * 16384
+        rows.append({"probe": label, "pages": pages, "pages_per_item": per_item,
+                     "heads_per_workgroup": heads, "groups_in_flight": depth, "mode": mode,
+                     "workgroups": pages // per_item * (8 // heads),
+                     "cold_us": round(cold, 2), "cold_gbps": round(nbytes / cold / 1e3, 1),
+                     "hot_us": round(hot, 2), "hot_gbps": round(nbytes / hot / 1e3, 1)})
+    kernel = {}
+    for state, before in (("cold", scrub), ("hot", None)):
+        for _ in range(3):
+            if before is not None:
+                before()
+            bound()
+        kernel[state] = round(1e3 * statistics.fmean(kernel_samples(torch, bound, samples, before)), 2)
+    pages = int(w.old_indices.numel())
+    best_cold = min(r["cold_us"] / r["pages"] for r in rows) * pages
+    pattern_cold = rows[0]["cold_us"] / rows[0]["pages"] * pages
+    return {"metric": "load-only stream of the B1/49K INT8 pages vs the decode partial kernel",
+            "unit": "us", "probes": rows,
+            "decode_partial_kernel_us": kernel,
+            "int8_pages": pages,
+            "kernel_over_own_pattern_cold": round(pattern_cold / kernel["cold"], 4),
+            "kernel_over_best_probe_cold": round(best_cold / kernel["cold"], 4),
+            "note": "probe times scaled to the kernel's 3056 INT8 pages for the ratios; the kernel "
+                    "also streams 16 FP16 tail pages (1 MB) and computes"}
+
+
 PILOT_SPLITS = (0, 8, 16, 28, 48, 64)
 
 
@@ -957,6 +1038,9 @@ def main() -> int:
         return 0
     if args.pilot:
         print(json.dumps(pilot_sweep(torch, decode, workloads, device, scrub_clean)), flush=True)
+        return 0
+    if args.stream_probe:
+        print(json.dumps(stream_probe(torch, w, bound, scrub_clean)), flush=True)
         return 0
 
     # contract timed region: K cold steps bracketed by synchronize

@@ -548,6 +548,19 @@ int32_t pg_probe_linear_read(const void* src, int64_t bytes, int32_t* sink, int3
 int32_t pg_probe_page_walk(const void* k_pages, const void* v_pages, const int32_t* indices,
                            int32_t pages, int32_t pages_per_block, int32_t page_bytes,
                            int32_t* sink, void* start_event, void* stop_event, void* stream);
+/* Reads pages indices[0..pages) the way the INT8 decode kernel does, loads
+ * only: work items of ``pages_per_item`` consecutive entries (4..64, a
+ * multiple of 4, dividing ``pages``), one wave per KV head (8 KV heads of
+ * 128 codes, 16 KiB pages), ``heads_per_block`` (4 or 8) waves per
+ * workgroup, 4-page groups with ``depth`` (1 or 2) groups in flight per wave.
+ * ``mode`` 0 = the decode kernel's lane pattern, 1 = whole 128-byte head
+ * rows per lane group, 2 = whole pages as contiguous 1 KiB per instruction
+ * (heads_per_block 8).  Gives the stream rate of the decode's own access
+ * pattern, to set the decode kernel against. */
+int32_t pg_probe_decode_walk(const void* k_pages, const void* v_pages, const int32_t* indices,
+                             int32_t pages, int32_t pages_per_item, int32_t heads_per_block,
+                             int32_t depth, int32_t mode, int32_t* sink, void* start_event,
+                             void* stop_event, void* stream);
 
 #ifdef __cplusplus
 }

@@ -116,6 +116,7 @@ PROTOTYPES = {
                                           _i32, _f32, _p]),
     "pg_probe_linear_read": (_i32, [_p, _i64, _p, _i32, _p, _p, _p]),
     "pg_probe_page_walk": (_i32, [_p, _p, _p, _i32, _i32, _i32, _p, _p, _p, _p]),
+    "pg_probe_decode_walk": (_i32, [_p, _p, _p, _i32, _i32, _i32, _i32, _i32, _p, _p, _p, _p]),
 }
 
 _lock = threading.Lock()

@@ -6,7 +6,12 @@
 //    16 bytes per lane per load, eight nontemporal loads in flight per lane;
 //  * page_walk_kernel: the pages of a CSR page table (any order), each read
 //    as one contiguous block of K codes and one of V codes by a whole
-//    workgroup (the most favourable way to stream this cache's layout).
+//    workgroup (the most favourable way to stream this cache's layout);
+//  * decode_walk_kernel: the same pages read the way the INT8 decode kernel
+//    reads them (work items of consecutive table entries, one wave per KV
+//    head, 4-page groups with 1 or 2 groups in flight), loads only, so
+//    that the decode kernel can be set against the stream of its own
+//    access pattern; ``mode`` varies the lane pattern of the loads.
 // Loaded values are folded into a register and written only under a
 // condition that depends on them, so no load can be removed.
 #include "pg_common.h"
@@ -57,6 +62,113 @@ __global__ __launch_bounds__(kProbeThreads) void page_walk_kernel(const int8_t* 
   if ((acc.x ^ acc.y ^ acc.z ^ acc.w) == 0x5a17c3e1) sink[blockIdx.x] = acc.x;
 }
 
+// Loads of one 4-page group for one wave: 8 x 16 B of K and 16 x 8 B of V
+// per lane (the decode kernel's register footprint).
+struct WalkGroup {
+  v4i k[4][2];
+  uint32_t v[16][2];
+};
+
+template <typename T>
+__device__ __forceinline__ void walk_pin(T& x) {
+  T value = x;
+  asm volatile("" : "+v"(value));
+  x = value;
+}
+
+// Work item b covers table entries [b * pages_per_item, +pages_per_item);
+// wave w of workgroup (b, y) reads KV head y * heads_per_block + w.  Lane
+// (kg = lane / 16, m16 = lane % 16) offsets within a (page, head), for 8 KV
+// heads of 128 codes (1 KiB rows):
+//   mode 0 (the decode kernel's): K bytes 16 kg.. and 64 + 16 kg.. of token
+//          row m16; V 8 bytes of dims 8 m16.. of token rows 4 kg + t;
+//   mode 1: whole 128-byte head rows, 8 rows per instruction;
+//   mode 2: the workgroup's waves read whole pages as contiguous 1 KiB per
+//          instruction (every byte of the page once; heads_per_block 8).
+template <int kDepth, int kMode>
+__global__ __launch_bounds__(512) void decode_walk_kernel(const int8_t* k_pages,
+                                                          const int8_t* v_pages,
+                                                          const int32_t* indices,
+                                                          int32_t pages_per_item,
+                                                          int32_t heads_per_block, int32_t* sink) {
+  const int wave = threadIdx.x / kWave;
+  const int lane = threadIdx.x % kWave;
+  const int head = blockIdx.y * heads_per_block + wave;
+  const int m16 = lane & 15;
+  const int kg = lane >> 4;
+  const int begin = blockIdx.x * pages_per_item;
+  const int my_page = indices[begin + min(lane, pages_per_item - 1)];
+  const uint32_t k_off = kMode == 0 ? m16 * 1024 + head * 128 + 16 * kg
+                         : kMode == 1 ? (lane >> 3) * 1024 + head * 128 + 16 * (lane & 7)
+                                      : wave * 2048 + 16 * lane;
+  const uint32_t k_step = kMode == 0 ? 64 : kMode == 1 ? 8192 : 1024;
+  const uint32_t v_off = kMode == 0 ? 4 * kg * 1024 + head * 128 + 8 * m16 : k_off;
+  v4i acc = {0, 0, 0, 0};
+  WalkGroup buf[kDepth];
+  auto issue = [&](int g, WalkGroup& d) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int64_t p = __builtin_amdgcn_readlane(my_page, 4 * g + i);
+      const int8_t* kp = k_pages + p * 16384;
+      d.k[i][0] = *reinterpret_cast<const v4i*>(kp + k_off);
+      d.k[i][1] = *reinterpret_cast<const v4i*>(kp + k_off + k_step);
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int64_t p = __builtin_amdgcn_readlane(my_page, 4 * g + i);
+      const int8_t* vp = v_pages + p * 16384;
+      if (kMode == 0) {
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+          const uint2 x = *reinterpret_cast<const uint2*>(vp + v_off + t * 1024);
+          d.v[4 * i + t][0] = x.x;
+          d.v[4 * i + t][1] = x.y;
+        }
+      } else {
+        const v4i a0 = *reinterpret_cast<const v4i*>(vp + v_off);
+        const v4i a1 = *reinterpret_cast<const v4i*>(vp + v_off + k_step);
+        d.v[4 * i][0] = a0.x;
+        d.v[4 * i][1] = a0.y;
+        d.v[4 * i + 1][0] = a0.z;
+        d.v[4 * i + 1][1] = a0.w;
+        d.v[4 * i + 2][0] = a1.x;
+        d.v[4 * i + 2][1] = a1.y;
+        d.v[4 * i + 3][0] = a1.z;
+        d.v[4 * i + 3][1] = a1.w;
+      }
+    }
+  };
+  auto consume = [&](WalkGroup& c) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      walk_pin(c.k[i][0]);
+      walk_pin(c.k[i][1]);
+      acc ^= c.k[i][0] ^ c.k[i][1];
+    }
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      walk_pin(c.v[i][0]);
+      walk_pin(c.v[i][1]);
+      acc.x ^= static_cast<int>(c.v[i][0]);
+      acc.y ^= static_cast<int>(c.v[i][1]);
+    }
+  };
+  const int groups = pages_per_item / 4;
+#pragma unroll
+  for (int d = 0; d < kDepth; ++d)
+    if (d < groups) issue(d, buf[d]);
+  for (int g = 0; g < groups; g += kDepth) {
+#pragma unroll
+    for (int d = 0; d < kDepth; ++d) {
+      if (g + d < groups) {
+        consume(buf[d]);
+        if (g + d + kDepth < groups) issue(g + d + kDepth, buf[d]);
+      }
+    }
+  }
+  if ((acc.x ^ acc.y ^ acc.z ^ acc.w) == 0x5a17c3e1) sink[blockIdx.x] = acc.x;
+}
+
 }  // namespace
 }  // namespace pg
 
@@ -87,6 +199,42 @@ extern "C" int32_t pg_probe_linear_read(const void* src, int64_t bytes, int32_t*
   if (blocks < 1) return fail(PG_ERROR_INVALID_ARGUMENT, "blocks must be positive");
   return probe_launch(linear_read_kernel, blocks, stream, start_event, stop_event,
                       "probe_linear_read", static_cast<const v4i*>(src), bytes / 16, sink);
+}
+
+extern "C" int32_t pg_probe_decode_walk(const void* k_pages, const void* v_pages,
+                                        const int32_t* indices, int32_t pages,
+                                        int32_t pages_per_item, int32_t heads_per_block,
+                                        int32_t depth, int32_t mode, int32_t* sink,
+                                        void* start_event, void* stop_event, void* stream) {
+  clear_error();
+  if (!k_pages || !v_pages || !indices || !sink)
+    return fail(PG_ERROR_INVALID_ARGUMENT, "null tensor pointer");
+  if (pages_per_item < 4 || pages_per_item > 64 || pages_per_item % 4 || pages < pages_per_item ||
+      pages % pages_per_item)
+    return fail(PG_ERROR_INVALID_ARGUMENT,
+                "pages must be whole items of 4..64 pages (a multiple of 4 each)");
+  if (heads_per_block != 4 && heads_per_block != 8)
+    return fail(PG_ERROR_INVALID_ARGUMENT, "heads_per_block must be 4 or 8 (of 8 KV heads)");
+  if (depth < 1 || depth > 2) return fail(PG_ERROR_INVALID_ARGUMENT, "depth must be 1 or 2");
+  if (mode < 0 || mode > 2 || (mode == 2 && heads_per_block != 8))
+    return fail(PG_ERROR_INVALID_ARGUMENT, "mode must be 0, 1, or 2 with 8 heads per block");
+  const dim3 grid(pages / pages_per_item, 8 / heads_per_block);
+  const dim3 block(kWave * heads_per_block);
+  hipEvent_t start = static_cast<hipEvent_t>(start_event);
+  hipEvent_t stop = static_cast<hipEvent_t>(stop_event);
+  const int8_t* k = static_cast<const int8_t*>(k_pages);
+  const int8_t* v = static_cast<const int8_t*>(v_pages);
+#define PG_WALK_CASE(D, M)                                                                    \
+  if (depth == D && mode == M) {                                                             \
+    hipExtLaunchKernelGGL((decode_walk_kernel<D, M>), grid, block, 0, as_stream(stream), start, \
+                          stop, 0, k, v, indices, pages_per_item, heads_per_block, sink);      \
+    return check_launch("probe_decode_walk");                                                \
+  }
+  PG_WALK_CASE(1, 0) PG_WALK_CASE(2, 0)
+  PG_WALK_CASE(1, 1) PG_WALK_CASE(2, 1)
+  PG_WALK_CASE(1, 2) PG_WALK_CASE(2, 2)
+#undef PG_WALK_CASE
+  return fail(PG_ERROR_INVALID_ARGUMENT, "unsupported probe configuration");
 }
 
 extern "C" int32_t pg_probe_page_walk(const void* k_pages, const void* v_pages,

@@ -228,3 +228,22 @@ def test_page_id_check_is_opt_in(monkeypatch):
         decode._check_page_ids(span, 7, "INT8")
     with pytest.raises(ValueError, match="span \\[-1, 3\\]"):
         decode._check_page_ids((-1, 3), 8, "exact")
+
+
+@pytest.mark.parametrize("args,message", [
+    ((0, 16, 16, 4, 4, 1, 0), "null tensor pointer"),
+    ((16, 16, 6, 4, 2, 1, 0), "whole items"),          # pages_per_item not a multiple of 4
+    ((16, 18, 8, 4, 2, 1, 0), "whole items"),          # pages not whole items
+    ((16, 16, 16, 2, 2, 1, 0), "heads_per_block"),
+    ((16, 16, 16, 8, 3, 1, 0), "depth"),
+    ((16, 16, 16, 4, 2, 2, 0), "mode"),                # whole pages need 8 heads per block
+])
+def test_decode_walk_probe_rejects(args, message):
+    """Argument checks of pg_probe_decode_walk run before any launch (no GPU
+    needed); fake non-null pointers never reach a kernel."""
+    lib = _capi.library()
+    ptr, pages, per_item, heads, depth, mode, _ = args
+    fake = ptr or None
+    rc = lib.pg_probe_decode_walk(fake, fake, fake, pages, per_item, heads, depth, mode, fake,
+                                  None, None, None)
+    assert rc == 1 and message in _capi.last_error()

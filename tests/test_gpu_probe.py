@@ -35,3 +35,18 @@ def test_probes_read_and_time_themselves(cuda):
     assert "16-byte" in _capi.last_error()
     assert lib.pg_probe_page_walk(None, None, None, 1, 1, 16, sink.data_ptr(), None, None,
                                   stream) == 1
+
+
+def test_decode_walk_probe_reads_in_every_mode(cuda):
+    lib = _capi.library()
+    stream = torch.cuda.current_stream().cuda_stream
+    pages = torch.zeros(16, 16, 8, 128, dtype=torch.int8, device=cuda)
+    ids = torch.randperm(16, dtype=torch.int32).to(cuda)
+    sink = torch.full((64,), 7, dtype=torch.int32, device=cuda)
+    for per_item, heads, depth, mode in ((4, 4, 1, 0), (8, 4, 2, 0), (16, 8, 2, 0), (8, 4, 2, 1),
+                                         (8, 8, 1, 2)):
+        assert lib.pg_probe_decode_walk(pages.data_ptr(), pages.data_ptr(), ids.data_ptr(), 16,
+                                        per_item, heads, depth, mode, sink.data_ptr(), None, None,
+                                        stream) == 0, _capi.last_error()
+    torch.cuda.synchronize()
+    assert bool((sink == 7).all())
