@@ -127,6 +127,27 @@ class LibraryMissingError(RuntimeError):
     pass
 
 
+def load_library(path):
+    """A ctypes handle of the library at ``path`` with every prototype set
+    and its ABI checked (not cached; ``library()`` holds the product's).
+    Alternative builds (``python -m pagegauge_amd.build --variant NAME``)
+    load beside the product this way."""
+    if not Path(path).exists():
+        raise LibraryMissingError(
+            f"{path} is missing: build it with `python -c "
+            "'import __graft_entry__ as g; g.build()'` (hipcc, gfx950)")
+    lib = ctypes.CDLL(str(path))
+    for name, (restype, argtypes) in PROTOTYPES.items():
+        fn = getattr(lib, name)
+        fn.restype = restype
+        fn.argtypes = argtypes
+    version = lib.pg_abi_version()
+    if version != ABI_VERSION:
+        raise LibraryMissingError(
+            f"{Path(path).name} ABI {version} does not match the bindings ({ABI_VERSION})")
+    return lib
+
+
 def library():
     """Load (once) and return the ctypes handle; raises if the build is absent."""
     global _library
@@ -134,20 +155,7 @@ def library():
         return _library
     with _lock:
         if _library is None:
-            if not LIBRARY_PATH.exists():
-                raise LibraryMissingError(
-                    f"{LIBRARY_PATH} is missing: build it with `python -c "
-                    "'import __graft_entry__ as g; g.build()'` (hipcc, gfx950)")
-            lib = ctypes.CDLL(str(LIBRARY_PATH))
-            for name, (restype, argtypes) in PROTOTYPES.items():
-                fn = getattr(lib, name)
-                fn.restype = restype
-                fn.argtypes = argtypes
-            version = lib.pg_abi_version()
-            if version != ABI_VERSION:
-                raise LibraryMissingError(
-                    f"libpagegauge_hip.so ABI {version} does not match the bindings ({ABI_VERSION})")
-            _library = lib
+            _library = load_library(LIBRARY_PATH)
     return _library
 
 
