@@ -863,7 +863,16 @@ STREAM_PROBES = (
 )
 
 
-def stream_probe(torch, w, bound, scrub, samples: int = 20):
+STREAM_PROBES_16K = (
+    ("decode pattern, 8-page items, 4 heads per workgroup", 1008, 8, 4, 2, 0),
+    ("decode pattern, 12-page items, 4 heads per workgroup", 1008, 12, 4, 2, 0),
+    ("decode pattern, 4-page items, 4 heads per workgroup", 1008, 4, 4, 1, 0),
+    ("whole pages per workgroup, 8-page items", 1008, 8, 8, 2, 2),
+    ("whole pages per workgroup, 4-page items", 1008, 4, 8, 1, 2),
+)
+
+
+def stream_probe(torch, w, bound, scrub, samples: int = 20, probes=STREAM_PROBES):
     """Load-only walks of the B1/49K INT8 pages (pg_probe_decode_walk) in the
     decode kernel's access pattern and in more favourable ones, cold (after
     the clean scrub) and hot, beside the decode's partial kernel timed the
@@ -893,7 +902,7 @@ def stream_probe(torch, w, bound, scrub, samples: int = 20):
         return 1e3 * statistics.fmean(a.elapsed_time(b) for a, b in events)
 
     rows = []
-    for label, pages, per_item, heads, depth, mode in STREAM_PROBES:
+    for label, pages, per_item, heads, depth, mode in probes:
         def walk(start, stop, pages=pages, per_item=per_item, heads=heads, depth=depth, mode=mode):
             _capi.check(lib.pg_probe_decode_walk(
                 w.k_codes.data_ptr(), w.v_codes.data_ptr(), w.old_indices.data_ptr(), pages,
@@ -915,7 +924,7 @@ def stream_probe(torch, w, bound, scrub, samples: int = 20):
     pages = int(w.old_indices.numel())
     best_cold = min(r["cold_us"] / r["pages"] for r in rows) * pages
     pattern_cold = rows[0]["cold_us"] / rows[0]["pages"] * pages
-    return {"metric": "load-only stream of the B1/49K INT8 pages vs the decode partial kernel",
+    return {"metric": "load-only stream of the INT8 pages vs the decode partial kernel",
             "unit": "us", "probes": rows,
             "decode_partial_kernel_us": kernel,
             "int8_pages": pages,
@@ -1040,7 +1049,17 @@ def main() -> int:
         print(json.dumps(pilot_sweep(torch, decode, workloads, device, scrub_clean)), flush=True)
         return 0
     if args.stream_probe:
-        print(json.dumps(stream_probe(torch, w, bound, scrub_clean)), flush=True)
+        result = {"b1_49k": stream_probe(torch, w, bound, scrub_clean)}
+        # the config-5 decoder's per-layer shape: 16K context (1008 INT8 pages + the ring)
+        w16 = workloads.build_decode_workload([16384 + 16], args.seed, device=device)
+        d16 = decode.PageGaugeSegmentedDecode(torch.empty(64 << 20, dtype=torch.uint8, device=device))
+        d16.plan(w16.old_indptr, w16.old_indices, w16.old_last_page_len, w16.tail_indptr,
+                 w16.tail_indices, w16.tail_last_page_len)
+        b16 = d16.bind(w16.query, (w16.k_codes, w16.v_codes), w16.k_scale, w16.v_scale,
+                       (w16.tail_k, w16.tail_v), w16.value_center, out=torch.empty_like(w16.query),
+                       lse=torch.empty(1, 32, dtype=torch.float32, device=device))
+        result["b1_16k"] = stream_probe(torch, w16, b16, scrub_clean, probes=STREAM_PROBES_16K)
+        print(json.dumps(result), flush=True)
         return 0
 
     # contract timed region: K cold steps bracketed by synchronize
