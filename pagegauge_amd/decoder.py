@@ -408,9 +408,11 @@ class SegmentTable:
     """Device page table of one decode segment with a structural-signature
     guard (``GraphDecodeWrapper.plan``, scripts/benchmark_page_gauge_transformer.py:1517-1580).
 
-    ``plan`` always refreshes the device ``last_len`` (the kernels re-read it
-    on every run, so a captured graph stays valid across the 16 steps of a
-    page) and rewrites indptr/indices only when the signature changes.  The
+    ``plan`` keeps the device ``last_len`` current (the kernels re-read it on
+    every run, so a captured graph stays valid across the 16 steps of a page);
+    it launches the fill only when the value changes, since every fill between
+    two graph replays is a launch the GPU waits for.  indptr/indices are
+    rewritten only when the signature changes.  The
     signature is (batch, pages per request, split, table storage, epoch): the
     work list of the split scheduler depends on page counts only, not on the
     number of tokens in the last page.  Returns True when the table changed.
@@ -421,6 +423,7 @@ class SegmentTable:
         self.indptr = torch.empty(batch_size + 1, device=device, dtype=torch.int32)
         self.indices = torch.empty(batch_size * max_pages, device=device, dtype=torch.int32)
         self.last_len = torch.full((batch_size,), PAGE, device=device, dtype=torch.int32)
+        self._device_last_len = PAGE     # the value ``last_len`` holds on the device
         self.host_indptr: Optional[torch.Tensor] = None
         self.host_last_len: Optional[torch.Tensor] = None
         self.signature: Optional[tuple] = None
@@ -451,8 +454,10 @@ class SegmentTable:
         total = self.batch_size * pages
         if total > self.indices.numel():
             raise ValueError("decode segment exceeds the allocated page table")
-        self.last_len.fill_(last_page_len)
-        self.last_len_fills += 1
+        if last_page_len != self._device_last_len:
+            self.last_len.fill_(last_page_len)
+            self._device_last_len = last_page_len
+            self.last_len_fills += 1
         self.host_last_len = torch.full((self.batch_size,), last_page_len, dtype=torch.int32)
         signature = (self.batch_size, pages, int(split_pages), physical_indices.data_ptr(),
                      page_table_epoch)
