@@ -934,6 +934,46 @@ def stream_probe(torch, w, bound, scrub, samples: int = 20, probes=STREAM_PROBES
                     "also streams 16 FP16 tail pages (1 MB) and computes"}
 
 
+# weight bytes of the config-5 decoder's projections (FP16 [rows, k])
+DECODER_WEIGHTS = (("gate_up", 28672, 4096), ("down", 4096, 14336), ("qkv", 6144, 4096),
+                   ("o", 4096, 4096), ("lm_head", 32768, 4096))
+
+
+def weight_read_ceiling(torch, device, scrub, samples: int = 10):
+    """Cold (after the clean scrub) nontemporal linear reads of each decoder
+    projection's weight bytes (pg_probe_linear_read, best launch shape, mean
+    of dispatch-stamped durations): the ceiling of the projection kernels,
+    which read every weight byte once per step with the same loads."""
+    from pagegauge_amd import _capi
+
+    lib = _capi.library()
+    stream = torch.cuda.current_stream().cuda_stream
+    sink = torch.empty(1 << 16, dtype=torch.int32, device=device)
+    events = [[torch.cuda.Event(enable_timing=True) for _ in range(2)] for _ in range(samples)]
+    for pair in events:
+        for e in pair:
+            e.record()
+    torch.cuda.synchronize()
+    out = {}
+    for name, rows, k in DECODER_WEIGHTS:
+        nbytes = rows * k * 2
+        buf = torch.ones(nbytes // 4, dtype=torch.int32, device=device)
+        best = None
+        for blocks in (512, 1024, 2048, 4096, 8192):
+            for a, b in events:
+                scrub()
+                _capi.check(lib.pg_probe_linear_read(buf.data_ptr(), nbytes, sink.data_ptr(), blocks,
+                                                     a.cuda_event, b.cuda_event, stream), "probe")
+            torch.cuda.synchronize()
+            t = 1e3 * statistics.fmean(a.elapsed_time(b) for a, b in events)
+            best = t if best is None else min(best, t)
+        out[name] = {"bytes": nbytes, "cold_read_us": round(best, 2),
+                     "cold_read_gbps": round(nbytes / best / 1e3, 1)}
+        del buf
+    torch.cuda.empty_cache()
+    return out
+
+
 PILOT_SPLITS = (0, 8, 16, 28, 48, 64)
 
 
@@ -1059,6 +1099,8 @@ def main() -> int:
                        (w16.tail_k, w16.tail_v), w16.value_center, out=torch.empty_like(w16.query),
                        lse=torch.empty(1, 32, dtype=torch.float32, device=device))
         result["b1_16k"] = stream_probe(torch, w16, b16, scrub_clean, probes=STREAM_PROBES_16K)
+        del w16, d16, b16
+        result["decoder_weight_reads"] = weight_read_ceiling(torch, device, scrub_clean)
         print(json.dumps(result), flush=True)
         return 0
 
