@@ -872,6 +872,13 @@ STREAM_PROBES_16K = (
 )
 
 
+STREAM_PROBES_4K = (
+    ("decode pattern, 4-page items, 4 heads per workgroup, 1 group in flight", 240, 4, 4, 1, 0),
+    ("decode pattern, 8-page items, 4 heads per workgroup", 240, 8, 4, 2, 0),
+    ("whole pages per workgroup, 4-page items, 1 group in flight", 240, 4, 8, 1, 2),
+)
+
+
 def stream_probe(torch, w, bound, scrub, samples: int = 20, probes=STREAM_PROBES):
     """Load-only walks of the B1/49K INT8 pages (pg_probe_decode_walk) in the
     decode kernel's access pattern and in more favourable ones, cold (after
@@ -1100,6 +1107,16 @@ def main() -> int:
                        lse=torch.empty(1, 32, dtype=torch.float32, device=device))
         result["b1_16k"] = stream_probe(torch, w16, b16, scrub_clean, probes=STREAM_PROBES_16K)
         del w16, d16, b16
+        # config 1: 4096 tokens (240 INT8 pages + the ring)
+        w4 = workloads.single_4k(args.seed, device=device)
+        d4 = decode.PageGaugeSegmentedDecode(torch.empty(64 << 20, dtype=torch.uint8, device=device))
+        d4.plan(w4.old_indptr, w4.old_indices, w4.old_last_page_len, w4.tail_indptr,
+                w4.tail_indices, w4.tail_last_page_len)
+        b4 = d4.bind(w4.query, (w4.k_codes, w4.v_codes), w4.k_scale, w4.v_scale,
+                     (w4.tail_k, w4.tail_v), w4.value_center, out=torch.empty_like(w4.query),
+                     lse=torch.empty(1, 32, dtype=torch.float32, device=device))
+        result["config1_4k"] = stream_probe(torch, w4, b4, scrub_clean, probes=STREAM_PROBES_4K)
+        del w4, d4, b4
         result["decoder_weight_reads"] = weight_read_ceiling(torch, device, scrub_clean)
         print(json.dumps(result), flush=True)
         return 0
