@@ -192,3 +192,30 @@ def test_exact_tail_hint_is_checked():
         plan_work_items([0, 100], [16], exact_tail_pages_hint=16)
     with pytest.raises(RuntimeError, match="must be non-negative"):
         plan_work_items([0, 100], [16], kv_data_type="heterogeneous", exact_tail_pages_hint=-1)
+
+
+try:
+    from hypothesis import given, settings, strategies as st
+except ImportError:                                  # pragma: no cover
+    given = None
+
+if given is not None:
+    @settings(max_examples=120, deadline=None)
+    @given(old=st.lists(st.integers(0, 900), min_size=1, max_size=12),
+           tail=st.data(), split=st.sampled_from([None, 1, 3, 4, 16, 64]),
+           last=st.data())
+    def test_random_batches_cover_every_page_once(old, tail, split, last):
+        """Fuzzed batches (empty and one-page segments included): the planner
+        covers every INT8 and tail page exactly once, within the 64-page cap,
+        with each request's items contiguous, numbered in order and tail
+        first, and a workgroup shape that divides the 8 KV heads."""
+        tails = tail.draw(st.lists(st.integers(0, 16), min_size=len(old), max_size=len(old)))
+        lasts = last.draw(st.lists(st.integers(1, 16), min_size=len(old), max_size=len(old)))
+        if sum(old) + sum(tails) == 0:
+            return
+        plan, items, ptr = plan_work_items(_indptr(old), lasts, _indptr(tails), lasts,
+                                           split_pages=split or 0)
+        assert plan.num_items == items.shape[0] == ptr[-1]
+        _check_cover(items, ptr.tolist(), old, tails)
+        assert plan.max_items_per_request == max(int(ptr[b + 1] - ptr[b]) for b in range(len(old)))
+        assert plan.waves_per_block in (1, 2, 4, 8) and 8 % plan.waves_per_block == 0
