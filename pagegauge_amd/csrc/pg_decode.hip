@@ -622,10 +622,19 @@ __device__ void finalize_page(const DecodeArgs& a, int request, int page, int kv
   }
 }
 
+// kStrided: ``subs`` waves share one (request, KV head), and wave ``sub``
+// takes pages sub, sub + subs, ... of the range into its own state (the
+// caller merges the states); otherwise the wave takes every page.
+template <bool kStrided = false>
 __device__ __forceinline__ void fp16_pages(const DecodeArgs& a, int request, const uint16_t* kpages,
                                            const uint16_t* vpages, const int32_t* indices,
                                            int begin, int end, int last_page, int last_len,
-                                           int kv, int lane, uint8_t* lds, HeadState& st) {
+                                           int kv, int lane, uint8_t* lds, HeadState& st,
+                                           int sub = 0, int subs = 1) {
+  if (!kStrided) {
+    sub = 0;
+    subs = 1;
+  }
   const int hkv = a.num_kv_heads;
   const int m16 = lane & 15;
   const int kg = lane >> 4;
@@ -656,8 +665,8 @@ __device__ __forceinline__ void fp16_pages(const DecodeArgs& a, int request, con
     v4u v[4];    // V: dims 8*m16 .. +7 of tokens 4*kg + k
   };
   Fp16Page buf[2];
-  auto issue = [&](int slot, Fp16Page& dst) {
-    const int page = __builtin_amdgcn_readlane(my_page, slot);
+  auto issue = [&](int local, Fp16Page& dst) {
+    const int page = __builtin_amdgcn_readlane(my_page, sub + local * subs);
     const uint16_t* kbase = kp + (static_cast<int64_t>(page) * kPageSize + m16) * row_stride + 8 * kg;
 #pragma unroll
     for (int j = 0; j < 4; ++j) dst.k[j] = *reinterpret_cast<const v8h*>(kbase + 32 * j);
@@ -682,7 +691,8 @@ __device__ __forceinline__ void fp16_pages(const DecodeArgs& a, int request, con
     }
   };
 
-  auto compute = [&](int slot, Fp16Page& cur) {
+  auto compute = [&](int local, Fp16Page& cur) {
+    const int slot = sub + local * subs;
 #pragma unroll
     for (int j = 0; j < 4; ++j) consume_point(cur.k[j]);
 #pragma unroll
@@ -736,15 +746,17 @@ __device__ __forceinline__ void fp16_pages(const DecodeArgs& a, int request, con
     }
   };
 
+  const int local_count = kStrided ? (count - sub + subs - 1) / subs : count;   // this wave's pages
+  if (kStrided && local_count <= 0) return;
   issue(0, buf[0]);
   int slot = 0;
-  for (; slot + 2 < count; slot += 2) {
+  for (; slot + 2 < local_count; slot += 2) {
     issue(slot + 1, buf[1]);
     compute(slot, buf[0]);
     issue(slot + 2, buf[0]);
     compute(slot + 1, buf[1]);
   }
-  if (slot + 1 < count) {
+  if (slot + 1 < local_count) {
     issue(slot + 1, buf[1]);
     compute(slot, buf[0]);
     compute(slot + 1, buf[1]);
@@ -1010,21 +1022,55 @@ struct TailMergeArgs {
   const uint16_t* value_center;
   int64_t center_batch_stride;
   int pages_per_request;
+  int subs;             // waves per KV head (each takes every subs-th page)
 };
 
+// One workgroup per (request, group of KV heads); ``subs`` waves per head walk
+// interleaved pages of the tail (the walk is latency-bound: a wave's pages
+// are a dependent chain of loads), and their states meet in LDS before the
+// merge with the old output.
 __global__ __launch_bounds__(kWave * kMaxWavesPerBlock) void tail_merge_kernel(TailMergeArgs t) {
   __shared__ __attribute__((aligned(16))) uint8_t lds_all[kMaxWavesPerBlock * kLdsPerWave];
+  __shared__ float sub_state[kMaxWavesPerBlock][10][kWave];
   const DecodeArgs& a = t.base;
   const int wave = threadIdx.x / kWave;
   const int lane = threadIdx.x % kWave;
   const int request = blockIdx.x;
-  const int kv = blockIdx.y * a.waves_per_block + wave;
+  const int head_slot = wave % a.waves_per_block;
+  const int sub = wave / a.waves_per_block;
+  const int kv = blockIdx.y * a.waves_per_block + head_slot;
   HeadState st;
   init_state(st);
   const int begin = request * t.pages_per_request;
   const int end = begin + t.pages_per_request;
-  fp16_pages(a, request, t.exact_k, t.exact_v, t.page_indices, begin, end, end - 1,
-             t.last_len[request], kv, lane, lds_all + wave * kLdsPerWave, st);
+  fp16_pages<true>(a, request, t.exact_k, t.exact_v, t.page_indices, begin, end, end - 1,
+                   t.last_len[request], kv, lane, lds_all + wave * kLdsPerWave, st, sub, t.subs);
+  if (t.subs > 1) {
+    sub_state[wave][0][lane] = st.m;
+    sub_state[wave][1][lane] = st.l;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) sub_state[wave][2 + i][lane] = st.o[i];
+    __syncthreads();
+    if (sub != 0) return;
+    float mx = st.m;
+    for (int j = 1; j < t.subs; ++j) mx = fmaxf(mx, sub_state[j * a.waves_per_block + head_slot][0][lane]);
+    float l = 0.0f;
+    float o[8] = {0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f};
+    if (mx != kNegInf) {
+      for (int j = 0; j < t.subs; ++j) {
+        const int w = j * a.waves_per_block + head_slot;
+        const float mj = sub_state[w][0][lane];
+        const float f = mj == kNegInf ? 0.0f : exp2f(mj - mx);
+        l += sub_state[w][1][lane] * f;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) o[i] += sub_state[w][2 + i][lane] * f;
+      }
+    }
+    st.m = mx;
+    st.l = l;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) st.o[i] = o[i];
+  }
   const float l_row = row16_sum(st.l);
   const int qh = kv * kGqa + (lane >> 4);
   const int n = lane & 15;
@@ -1713,7 +1759,10 @@ extern "C" int32_t pg_exact_tail_merge_center(const void* query, const void* exa
   t.base.query_batch_stride = static_cast<int64_t>(query_heads) * kHeadDim;
   t.base.num_qo_heads = query_heads;
   t.base.num_kv_heads = kv_heads;
-  t.base.waves_per_block = waves_per_block_for(kv_heads, int64_t{1} << 30, 1);
+  // one KV head per group of sub-waves: up to kMaxWavesPerBlock waves walk
+  // the tail's pages of one head in parallel
+  t.base.waves_per_block = 1;
+  t.subs = std::min(pages_per_request, kMaxWavesPerBlock);
   t.base.sm_scale_log2 = sm_scale * 1.4426950408889634f;
   t.exact_k = static_cast<const uint16_t*>(exact_key_pages);
   t.exact_v = static_cast<const uint16_t*>(exact_value_pages);
@@ -1725,7 +1774,7 @@ extern "C" int32_t pg_exact_tail_merge_center(const void* query, const void* exa
   t.center_batch_stride = center_batch_stride;
   t.pages_per_request = pages_per_request;
   const dim3 grid(batch_size, kv_heads / t.base.waves_per_block);
-  hipLaunchKernelGGL(tail_merge_kernel, grid, dim3(kWave * t.base.waves_per_block), 0,
+  hipLaunchKernelGGL(tail_merge_kernel, grid, dim3(kWave * t.base.waves_per_block * t.subs), 0,
                      as_stream(stream), t);
   return check_launch("exact_tail_merge_center");
 }
