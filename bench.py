@@ -380,6 +380,39 @@ def config4_inputs(torch):
             "v": [rnd(batch, 8, 128) for _ in range(steps)], "generator": gen}
 
 
+def exact_tail_merge_line(torch, device, scrub, samples: int = 40):
+    """The reference's fused exact-tail merge (``exact_tail_merge_center``,
+    tests/page_gauge_append_extension.cu:389-583) over full 16-page tails at
+    B = 1 and 8: cold p50 of the call (events around it, after the clean
+    scrub, which also covers the host's argument checks)."""
+    from pagegauge_amd import runtime
+
+    ext = runtime.load_append_extension()
+    out = {}
+    for batch in (1, 8):
+        gen = torch.Generator().manual_seed(20260840 + batch)
+        ring = 16
+        q = torch.randn(batch, 32, 128, generator=gen).half().to(device)
+        ek = (torch.randn(batch * ring, 16, 8, 128, generator=gen) * 0.35).half().to(device)
+        ev = (torch.randn(batch * ring, 16, 8, 128, generator=gen) * 0.35).half().to(device)
+        center = (torch.randn(batch, 8, 128, generator=gen) * 0.1).half().to(device)
+        idx = torch.randperm(batch * ring, generator=gen).to(torch.int32).to(device)
+        last = torch.full((batch,), 16, dtype=torch.int32, device=device)
+        old = torch.randn(batch, 32, 128, generator=gen).half().to(device)
+        lse = (torch.randn(batch, 32, generator=gen) + 8).float().to(device)
+
+        def call():
+            ext.exact_tail_merge_center(q, ek, ev, idx, last, old, lse,
+                                        center if batch > 1 else center[0], 128 ** -0.5)
+
+        for _ in range(3):
+            scrub()
+            call()
+        out[f"b{batch}"] = {"tail_pages": ring,
+                            "cold_call": summarize(call_samples(torch, call, samples, scrub))}
+    return out
+
+
 def update_config4(torch, device, replays: int):
     """Config 4 cache update: B=8, 16 decode steps (start lengths
     4096, 4099, ..., 16398: every row closes one page, four of them mid-window),
@@ -1180,6 +1213,7 @@ def main() -> int:
             torch.cuda.empty_cache()
         other["config3_b8_ragged"] = ragged
         other["config4_update"] = update_config4(torch, device, 50)
+        other["exact_tail_merge_center"] = exact_tail_merge_line(torch, device, scrub_clean)
         other["paper_b4_20k"] = paper_b4_20k(torch, decode, workloads, device, scrub_clean, 60)
     if not args.no_decoder:
         other = other or {}
