@@ -905,6 +905,12 @@ STREAM_PROBES_16K = (
 )
 
 
+STREAM_PROBES_B8 = (     # config 3, seed 20260840: its 8096 INT8 pages (the large plan)
+    ("decode pattern, 32-page items, 8 heads per workgroup", 8096, 32, 8, 2, 0),
+    ("decode pattern, 32-page items, 4 heads per workgroup", 8096, 32, 4, 2, 0),
+    ("whole pages per workgroup, 16-page items", 8096, 16, 8, 2, 2),
+)
+
 STREAM_PROBES_4K = (
     ("decode pattern, 4-page items, 4 heads per workgroup, 1 group in flight", 240, 4, 4, 1, 0),
     ("decode pattern, 8-page items, 4 heads per workgroup", 240, 8, 4, 2, 0),
@@ -1150,6 +1156,16 @@ def main() -> int:
                      lse=torch.empty(1, 32, dtype=torch.float32, device=device))
         result["config1_4k"] = stream_probe(torch, w4, b4, scrub_clean, probes=STREAM_PROBES_4K)
         del w4, d4, b4
+        # config 3 (first seed), the large plan
+        w8 = workloads.b8_ragged(workloads.VALIDATION_SEEDS[0], device=device)
+        d8 = decode.PageGaugeSegmentedDecode(torch.empty(64 << 20, dtype=torch.uint8, device=device))
+        d8.plan(w8.old_indptr, w8.old_indices, w8.old_last_page_len, w8.tail_indptr,
+                w8.tail_indices, w8.tail_last_page_len)
+        b8 = d8.bind(w8.query, (w8.k_codes, w8.v_codes), w8.k_scale, w8.v_scale,
+                     (w8.tail_k, w8.tail_v), w8.value_center, out=torch.empty_like(w8.query),
+                     lse=torch.empty(8, 32, dtype=torch.float32, device=device))
+        result["config3_b8_ragged"] = stream_probe(torch, w8, b8, scrub_clean, probes=STREAM_PROBES_B8)
+        del w8, d8, b8
         result["decoder_weight_reads"] = weight_read_ceiling(torch, device, scrub_clean)
         print(json.dumps(result), flush=True)
         return 0
