@@ -140,6 +140,62 @@ def kernel_samples(torch, bound, n, scrub=None):
     return [a.elapsed_time(b) for a, b in ev]
 
 
+def graph_call_samples(torch, bind, n, scrub):
+    """Whole-call durations (ms) of the call captured in a HIP graph and
+    replayed, the way the decoder's step graphs run the partial and combine
+    kernels.  ``bind(stream)`` returns the call bound to the capture stream;
+    the replay runs on the current stream between the two events, after the
+    untimed ``scrub``."""
+    stream = torch.cuda.Stream()
+    bound = bind(stream.cuda_stream)
+    stream.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(stream):
+        bound()                                    # eager warm-up on the capture stream
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=stream):
+        bound()
+    torch.cuda.synchronize()
+    for _ in range(3):
+        scrub()
+        graph.replay()
+    ev = [[torch.cuda.Event(enable_timing=True) for _ in range(2)] for _ in range(n)]
+    for i in range(n):
+        scrub()
+        ev[i][0].record()
+        graph.replay()
+        ev[i][1].record()
+    torch.cuda.synchronize()
+    return [a.elapsed_time(b) for a, b in ev]
+
+
+def graph_fixed_cost(torch, scrub, n: int = 40):
+    """Event-to-event p50 (µs) of one 1-element fill kernel launched eagerly
+    and as a one-node HIP graph, after the same untimed scrub: the cost a
+    graph replay adds independently of what it holds."""
+    tiny = torch.zeros(1, device=torch.cuda.current_device())
+    stream = torch.cuda.Stream()
+    stream.wait_stream(torch.cuda.current_stream())
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=stream):
+        tiny.zero_()
+    torch.cuda.synchronize()
+    result = {}
+    for name, fn in (("eager_fill_p50_us", tiny.zero_), ("graph_fill_p50_us", graph.replay)):
+        for _ in range(3):
+            scrub()
+            fn()
+        ev = [[torch.cuda.Event(enable_timing=True) for _ in range(2)] for _ in range(n)]
+        for i in range(n):
+            scrub()
+            ev[i][0].record()
+            fn()
+            ev[i][1].record()
+        torch.cuda.synchronize()
+        result[name] = round(1e3 * statistics.median([a.elapsed_time(b) for a, b in ev]), 3)
+    return result
+
+
 def timed_calls(torch, bound, n, scrub=None):
     """(partial kernel ms list, whole call ms list), n samples of each."""
     call = call_samples(torch, bound, n, scrub)
@@ -258,12 +314,17 @@ def decode_config(torch, decode, w, scrub, samples: int):
         scrub()
         bound()
     kernel, call = timed_calls(torch, bound, samples, scrub=scrub)
+    graph = graph_call_samples(
+        torch, lambda s: dec.bind(w.query, (w.k_codes, w.v_codes), w.k_scale, w.v_scale,
+                                  (w.tail_k, w.tail_v), w.value_center, out=out, lse=lse,
+                                  stream=s), samples, scrub)
     kernel_us = 1e3 * statistics.fmean(kernel)
     alg = w.algorithmic_bytes()
     return {
         "lengths": w.lengths if len(w.lengths) <= 8 else len(w.lengths),
         "work_items": dec.num_work_items,
         "call_p50_us": round(1e3 * statistics.median(call), 3),
+        "graph_call_p50_us": round(1e3 * statistics.median(graph), 3),
         "kernel_mean_us": round(kernel_us, 3),
         "algorithmic_bytes": alg,
         "achieved_gbps": round(alg / (kernel_us * 1e-6) / 1e9, 1),
@@ -1176,6 +1237,13 @@ def main() -> int:
     int8 = measure(torch, bound, args, scrub_clean, scrub_rmw)
     torch.cuda.synchronize()
     wall_s = time.perf_counter() - wall0
+    # the same call captured in a HIP graph (as the decoder's step graphs run it)
+    graph_ms = graph_call_samples(
+        torch, lambda s: dec.bind(w.query, (w.k_codes, w.v_codes), w.k_scale, w.v_scale,
+                                  (w.tail_k, w.tail_v), w.value_center, out=out, lse=lse,
+                                  stream=s), args.steps, scrub_clean)
+    int8["cold_clean_1gib_graph"] = {"call": summarize(graph_ms),
+                                     "fixed_cost": graph_fixed_cost(torch, scrub_clean)}
     bound()
     torch.cuda.synchronize()
     gpu_out = out.detach().cpu().numpy()
