@@ -1289,6 +1289,11 @@ def main() -> int:
     if not args.no_configs:
         other = {"config1_b1_4k": decode_config(torch, decode, workloads.single_4k(args.seed, device=device),
                                                 scrub_clean, 30)}
+        # B1/49K with the reference driver's own page table: physical pages in
+        # logical order (scripts/benchmark_flashinfer_page_affine_int8.py:463)
+        wi = workloads.b1_49k(args.seed, device=device, shuffle_pages=False)
+        other["b1_49k_identity_page_table"] = decode_config(torch, decode, wi, scrub_clean, 40)
+        del wi
         ragged = {}
         for seed in workloads.VALIDATION_SEEDS[:3]:
             wr = workloads.b8_ragged(seed, device=device)
