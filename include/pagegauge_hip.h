@@ -345,7 +345,7 @@ int32_t pg_decode_run(const pg_decode_plan_t* plan, const void* query,
 
 /* Run a PG_KV_HETEROGENEOUS plan: replaces the heterogeneous one-launch run
  * (scripts/page_gauge_heterogeneous_fa2.py:336-381, kernel
- * patches/flashinfer-0.6.17-page-gauge-heterogeneous-fa2.patch).  Entry j of
+ * patches/flashinfer-0.6.17-page-gauge-heterogeneous.patch).  Entry j of
  * request r's table (indices[indptr[r] + j]) indexes k_codes/v_codes (with
  * k_scale/v_scale) when j < old_kv_len[r] / 16 and exact_k/exact_v (FP16
  * centered pages) otherwise; old_kv_len (device int32 [B], page aligned) and
