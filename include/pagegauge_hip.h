@@ -306,12 +306,13 @@ int32_t pg_decode_plan(const int32_t* host_indptr, const int32_t* host_last_page
 
 /* The host half of pg_decode_plan (same arguments, same validation and
  * errors) without a device: fills *plan and, if items_out != NULL, the work
- * list as 8 int32 per item {request, kind (PG_KV_*), segment (0 primary,
+ * list as 12 int32 per item (items_capacity counts items, so items_out holds
+ * 12 * items_capacity int32) {request, kind (PG_KV_*), segment (0 primary,
  * 1 tail), page_begin, page_end (positions in indices/tail_indices), last
  * position of the segment, item index inside its request, items of the
- * request}; item_ptr_out
- * (if != NULL) receives [B+1] offsets of each request's items.  Call once
- * with items_out NULL to learn plan->num_items.  For inspection and tests of
+ * request, position of the request's first page in the segment, 3
+ * reserved}; item_ptr_out (if != NULL) receives [B+1] offsets of each
+ * request's items.  Call once with items_out NULL to learn plan->num_items.  For inspection and tests of
  * the scheduler; no reference counterpart (FlashInfer's plan info is opaque). */
 int32_t pg_decode_plan_host(const int32_t* host_indptr, const int32_t* host_last_page_len,
                             int32_t batch_size, int32_t primary_kind,

@@ -43,6 +43,7 @@ COMMON_FLAGS = [
 
 SOURCES = {
     "pg_error.cpp": [],
+    "pg_plan.cpp": [],
     "pg_update.hip": ["-ffp-contract=off"],
     "pg_decode.hip": [],
     "pg_decoder.hip": [],

@@ -7,23 +7,9 @@
 
 #include <string>
 
-#include "pagegauge_hip.h"
+#include "pg_host.h"
 
 namespace pg {
-
-constexpr int kHeadDim = 128;
-constexpr int kPageSize = 16;
-constexpr int kWave = 64;
-constexpr int kGqa = 4;  // query heads per KV head handled by the decode kernels
-
-// Records the message of a failing call for pg_last_error().
-void set_error(const std::string& message);
-void clear_error();
-
-inline int32_t fail(int32_t code, const std::string& message) {
-  set_error(message);
-  return code;
-}
 
 inline int32_t check_launch(const char* what) {
   hipError_t status = hipGetLastError();

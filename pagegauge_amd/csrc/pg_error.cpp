@@ -1,7 +1,7 @@
 // Thread-local error text for the C ABI (pg_last_error).
 #include <string>
 
-#include "pagegauge_hip.h"
+#include "pg_host.h"
 
 namespace pg {
 

@@ -1,0 +1,28 @@
+// Host-side definitions shared by every source of the library: the decode
+// shapes and the error reporting of the C ABI.  Plain C++ (no HIP), so the
+// host-only parts (the planner) also build with a host compiler.
+#pragma once
+
+#include <stdint.h>
+
+#include <string>
+
+#include "pagegauge_hip.h"
+
+namespace pg {
+
+constexpr int kHeadDim = 128;
+constexpr int kPageSize = 16;
+constexpr int kWave = 64;
+constexpr int kGqa = 4;  // query heads per KV head handled by the decode kernels
+
+// Records the message of a failing call for pg_last_error().
+void set_error(const std::string& message);
+void clear_error();
+
+inline int32_t fail(int32_t code, const std::string& message) {
+  set_error(message);
+  return code;
+}
+
+}  // namespace pg
