@@ -1,8 +1,10 @@
-"""The fused RoPE + centered append + completed-page finalize with head
-counts other than 32 query / 8 KV heads (the kernels take both at run
-time), bit-exact against the oracle: static and device-position ABIs over
-eight pages of tokens with a one-page exact prefix and a two-page ring (so
-the ring wraps and every page closes), and the FP16 baseline append."""
+"""The cache-update kernels with head counts other than 32 query / 8 KV
+heads (the kernels take both at run time): the fused RoPE + centered append
++ completed-page finalize, bit-exact against the oracle through the static
+and device-position ABIs over eight pages of tokens with a one-page exact
+prefix and a two-page ring (so the ring wraps and every page closes); the
+FP16 baseline append, bit-exact; and the fused exact-tail merge (GQA group
+4) within the reference test's tolerances."""
 
 from __future__ import annotations
 
@@ -90,3 +92,31 @@ def test_rope_append_fp16_any_head_count(ext, cuda, hq, hkv):
     assert_bit_equal(sq, host[0], "rotated query")
     assert_bit_equal(sk, host[1], "key pages")
     assert_bit_equal(sv, host[2], "value pages")
+
+
+@pytest.mark.parametrize("hq,hkv", HEADS)
+def test_exact_tail_merge_center_any_head_count(ext, cuda, hq, hkv):
+    from tests.helpers import max_abs
+
+    gen = torch.Generator().manual_seed(20260890 + hkv)
+    batch, ring_pages, tails = 2, 8, [117, 113]        # 8 ring pages each, ragged last page
+    q = _rand(gen, batch, hq, 128)
+    exact_k = _rand(gen, batch * ring_pages, 16, hkv, 128, scale=0.35)
+    exact_v = _rand(gen, batch * ring_pages, 16, hkv, 128, scale=0.35)
+    center = _rand(gen, batch, hkv, 128, scale=0.1)
+    pages = (max(tails) + 15) // 16
+    # every request names its 8 ring slots starting mid-ring
+    indices = torch.stack([r * ring_pages + (torch.arange(pages) + 5) % ring_pages
+                           for r in range(batch)]).reshape(-1).to(torch.int32)
+    last = torch.tensor([(t - 1) % 16 + 1 for t in tails], dtype=torch.int32)
+    old_out = _rand(gen, batch, hq, 128, scale=0.2)
+    old_lse = (torch.randn(batch, hq, generator=gen) * 0.5 + 8.0).float()
+    want_out, want_lse = oracle.exact_tail_merge_center(
+        q.numpy(), exact_k.numpy(), exact_v.numpy(), indices.numpy(), last.numpy(),
+        old_out.numpy(), old_lse.numpy(), center.numpy(), 128 ** -0.5)
+    dout, dlse = old_out.to(cuda), old_lse.to(cuda)
+    ext.exact_tail_merge_center(q.to(cuda), exact_k.to(cuda), exact_v.to(cuda), indices.to(cuda),
+                                last.to(cuda), dout, dlse, center.to(cuda), 128 ** -0.5)
+    torch.cuda.synchronize()
+    assert max_abs(dout, want_out) <= 2e-3
+    assert max_abs(dlse, want_lse) <= 2e-4
