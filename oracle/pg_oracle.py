@@ -26,7 +26,6 @@ reference tests' torch formulas run on the CPU, closed forms, or brute force.
 
 from __future__ import annotations
 
-import math
 from typing import Optional
 
 import numpy as np
