@@ -305,7 +305,7 @@ __global__ __launch_bounds__(kWave * kWaves) void decoder_gemv_kernel(GemvArgs a
   if (row0 < a.out_rows) load_rows<kR, kLoad, kC, kRope>(a, row0, wave, lane, wr);
   AppendInputs append_in{};
   if constexpr (kRope) {
-    // one row pair per workgroup (no grid-stride iterations)
+    // the row pair's RoPE / center inputs, loaded beside its weights
     if (threadIdx.x < kBatch && row0 < a.out_rows) append_in = append_inputs(a, threadIdx.x, row0 / 2);
   }
 
@@ -345,7 +345,12 @@ __global__ __launch_bounds__(kWave * kWaves) void decoder_gemv_kernel(GemvArgs a
 
   for (int it = 0; it < a.iterations; ++it, row0 += gridDim.x * kR) {
     if (row0 >= a.out_rows) break;                         // uniform over the block
-    if (it > 0) load_rows<kR, kLoad, kC, kRope>(a, row0, wave, lane, wr);
+    if (it > 0) {
+      load_rows<kR, kLoad, kC, kRope>(a, row0, wave, lane, wr);
+      if constexpr (kRope) {
+        if (threadIdx.x < kBatch) append_in = append_inputs(a, threadIdx.x, row0 / 2);
+      }
+    }
     float acc[kBatch][kLoad];
 #pragma unroll
     for (int b = 0; b < kBatch; ++b) {
@@ -579,10 +584,18 @@ __global__ __launch_bounds__(kArgmaxThreads) void argmax_kernel(const float* x, 
   }
 }
 
+#ifndef PG_QKV_MAX_BLOCKS
+#define PG_QKV_MAX_BLOCKS PG_GEMV_MAX_BLOCKS
+#endif
+
 template <int kBatch>
 int32_t launch_qkv_append(GemvArgs a, hipStream_t s) {
-  const int64_t blocks = a.out_rows / 2;      // one row pair per workgroup
-  a.iterations = 1;
+  // one row pair per workgroup and iteration; past the grid cap each
+  // workgroup takes several pairs (the input RMSNorm is then computed once
+  // per workgroup for all of them)
+  int64_t blocks = a.out_rows / 2;
+  a.iterations = static_cast<int>((blocks + PG_QKV_MAX_BLOCKS - 1) / PG_QKV_MAX_BLOCKS);
+  blocks = (blocks + a.iterations - 1) / a.iterations;
   hipLaunchKernelGGL((decoder_gemv_kernel<kBatch, 2, 2, false, true>),
                      dim3(static_cast<unsigned>(blocks)), dim3(kGemvThreads), 0, s, a);
   return check_launch("decoder_qkv_rope_append");
