@@ -338,6 +338,32 @@ def decode_config(torch, decode, w, scrub, samples: int):
 PAPER_B4_20K_RTX5090_US = {"segmented": 132.20, "heterogeneous": 143.06, "fp16": 220.75}
 
 
+def heterogeneous_call(torch, decode, w, device, out):
+    """The heterogeneous one-table decode of workload ``w`` as a callable
+    writing ``out``: one unified table per request (its INT8 pages, then its
+    FP16 ring pages, ``old_kv_len`` = the INT8 tokens), planned with the
+    exact-tail hint of the ring's 16 pages."""
+    old_ptr, tail_ptr = w.old_indptr.tolist(), w.tail_indptr.tolist()
+    old_idx, tail_idx = w.old_indices.cpu(), w.tail_indices.cpu()
+    rows, indptr, old_len = [], [0], []
+    for b in range(w.batch):
+        rows += [old_idx[old_ptr[b]:old_ptr[b + 1]], tail_idx[tail_ptr[b]:tail_ptr[b + 1]]]
+        indptr.append(indptr[-1] + old_ptr[b + 1] - old_ptr[b] + tail_ptr[b + 1] - tail_ptr[b])
+        old_len.append(16 * (old_ptr[b + 1] - old_ptr[b]))
+    unified = torch.cat(rows).to(device)
+    old_kv_len = torch.tensor(old_len, dtype=torch.int32, device=device)
+    het = decode.make_heterogeneous_page_gauge_wrapper(
+        None, torch.empty(64 << 20, dtype=torch.uint8, device=device))
+    het.plan(torch.tensor(indptr, dtype=torch.int32), unified, w.tail_last_page_len, 32, 8, 128, 16,
+             exact_tail_pages_hint=16)
+    args = (w.query, (w.k_codes, w.v_codes), w.k_scale, w.v_scale, w.tail_k, w.tail_v,
+            old_kv_len, w.value_center)
+    het.run(*args, out=out)                      # validates once
+    call = lambda: het.run(*args, out=out)       # noqa: E731
+    call.keep = (het, unified, old_kv_len)       # tables and workspace outlive the callable's use
+    return call
+
+
 def paper_b4_20k(torch, decode, workloads, device, scrub, samples: int):
     """The paper's B4 x 20K isolated-attention shape on this GPU: four
     requests of 20480 tokens (1264 INT8 + 16 FP16 pages each; the paper's
@@ -356,25 +382,8 @@ def paper_b4_20k(torch, decode, workloads, device, scrub, samples: int):
              w.tail_last_page_len)
     bounds["segmented"] = seg.bind(w.query, (w.k_codes, w.v_codes), w.k_scale, w.v_scale,
                                    (w.tail_k, w.tail_v), w.value_center, out=out, lse=lse)
-    # one unified table per request: its INT8 pages, then its FP16 ring pages
-    old_ptr, tail_ptr = w.old_indptr.tolist(), w.tail_indptr.tolist()
-    old_idx, tail_idx = w.old_indices.cpu(), w.tail_indices.cpu()
-    rows, indptr, old_len = [], [0], []
-    for b in range(w.batch):
-        rows += [old_idx[old_ptr[b]:old_ptr[b + 1]], tail_idx[tail_ptr[b]:tail_ptr[b + 1]]]
-        indptr.append(indptr[-1] + old_ptr[b + 1] - old_ptr[b] + tail_ptr[b + 1] - tail_ptr[b])
-        old_len.append(16 * (old_ptr[b + 1] - old_ptr[b]))
-    unified = torch.cat(rows).to(device)
-    old_kv_len = torch.tensor(old_len, dtype=torch.int32, device=device)
-    het = decode.make_heterogeneous_page_gauge_wrapper(
-        None, torch.empty(64 << 20, dtype=torch.uint8, device=device))
-    het.plan(torch.tensor(indptr, dtype=torch.int32), unified, w.tail_last_page_len, 32, 8, 128, 16,
-             exact_tail_pages_hint=16)
     out_h = torch.empty_like(w.query)
-    het_args = (w.query, (w.k_codes, w.v_codes), w.k_scale, w.v_scale, w.tail_k, w.tail_v,
-                old_kv_len, w.value_center)
-    het.run(*het_args, out=out_h)
-    bounds["heterogeneous"] = lambda: het.run(*het_args, out=out_h)
+    bounds["heterogeneous"] = heterogeneous_call(torch, decode, w, device, out_h)
     fp16 = decode.BatchDecodeWithPagedKVCacheWrapper(
         torch.empty(64 << 20, dtype=torch.uint8, device=device), "NHD")
     fp16.plan(w.fp16_indptr, w.fp16_indices, w.fp16_last_page_len, 32, 8, 128, 16,
@@ -1289,6 +1298,20 @@ def main() -> int:
     if not args.no_configs:
         other = {"config1_b1_4k": decode_config(torch, decode, workloads.single_4k(args.seed, device=device),
                                                 scrub_clean, 30)}
+        # B1/49K through the heterogeneous one-table decode (same pages)
+        out_h = torch.empty_like(w.query)
+        het = heterogeneous_call(torch, decode, w, device, out_h)
+        for _ in range(3):
+            scrub_clean()
+            het()
+        het_ms = call_samples(torch, het, 40, scrub_clean)
+        torch.cuda.synchronize()
+        other["b1_49k_heterogeneous"] = {
+            "call_p50_us": round(1e3 * statistics.median(het_ms), 3),
+            "segmented_call_p50_us": round(call_p50_us, 3),
+            "max_abs_vs_segmented": float(np.abs(out_h.cpu().numpy().astype(np.float32)
+                                                 - gpu_out.astype(np.float32)).max())}
+        del het, out_h
         # B1/49K with the reference driver's own page table: physical pages in
         # logical order (scripts/benchmark_flashinfer_page_affine_int8.py:463)
         wi = workloads.b1_49k(args.seed, device=device, shuffle_pages=False)
