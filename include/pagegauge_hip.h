@@ -269,12 +269,14 @@ enum { PG_KV_INT8 = 0, PG_KV_FP16 = 1, PG_KV_HETEROGENEOUS = 2 };
 int64_t pg_decode_workspace_bytes(int32_t batch_size, int32_t num_qo_heads,
                                   int64_t total_items, int64_t max_items_per_request);
 
-/* Split-count selection for 256-CU MI355X: pages per work item such that the
- * whole launch fills the GPU in (close to) whole waves of workgroups.
- * Replaces FlashInfer's automatic split (fixed_split_size=None) and the
- * capacity bound (2*num_SMs)//Hkv of
- * diagnostics/benchmark_sustained_dynamic_graphs.py:1497-1534.  bytes_per_page
- * is the per-(page, kv head) K+V traffic (4096 for INT8, 8192 for FP16). */
+/* Split selection: the pages per work item that pg_decode_plan's balanced
+ * planner (split_pages <= 0) chooses on num_cus CUs for batch_size requests
+ * sharing total_pages pages evenly, with no tail segment.  bytes_per_page is
+ * the per-(page, kv head) K+V traffic: 4096 plans INT8 pages, 8192 FP16
+ * pages.  Returns 0 (message in pg_last_error) for invalid arguments or a
+ * batch the planner cannot cut.  Replaces FlashInfer's automatic split
+ * (fixed_split_size=None) and the capacity bound (2*num_SMs)//Hkv of
+ * diagnostics/benchmark_sustained_dynamic_graphs.py:1497-1534. */
 int32_t pg_select_split_pages(int64_t total_pages, int32_t batch_size, int32_t num_kv_heads,
                               int32_t bytes_per_page, int32_t num_cus);
 

@@ -4,6 +4,7 @@
 #include "pg_plan.h"
 
 #include <algorithm>
+#include <climits>
 #include <cmath>
 #include <cstring>
 #include <string>
@@ -47,18 +48,36 @@ extern "C" int64_t pg_decode_workspace_bytes(int32_t batch_size, int32_t num_qo_
 extern "C" int32_t pg_select_split_pages(int64_t total_pages, int32_t batch_size,
                                          int32_t num_kv_heads, int32_t bytes_per_page,
                                          int32_t num_cus) {
-  // Pages per work item when the batch is spread over one workgroup per CU
-  // (a 512-thread block of eight KV-head waves holds a CU at two waves per
-  // SIMD), capped at one wave lane per page.  ``total_pages`` is in units of
-  // ``bytes_per_page``; pg_decode_plan applies the same rule per segment with
-  // nearly equal chunks.
-  (void)num_kv_heads;
-  (void)bytes_per_page;
-  if (total_pages <= 0) return 1;
-  if (num_cus <= 0) num_cus = 256;
-  const int64_t target_items = std::max<int64_t>(num_cus, batch_size);
-  const int64_t split = (total_pages + target_items - 1) / target_items;
-  return static_cast<int32_t>(std::min<int64_t>(std::max<int64_t>(split, 1), kMaxChunkPages));
+  // The balanced planner's pages per work item for ``batch_size`` requests
+  // sharing ``total_pages`` pages evenly (INT8 pages for 4096 bytes per
+  // (page, KV head) of K+V, FP16 pages for 8192), no tail segment.
+  clear_error();
+  if (total_pages <= 0 || batch_size <= 0 || num_kv_heads <= 0) {
+    fail(PG_ERROR_INVALID_ARGUMENT, "pages, batch size and KV heads must be positive");
+    return 0;
+  }
+  if (bytes_per_page != 4096 && bytes_per_page != 8192) {
+    fail(PG_ERROR_INVALID_ARGUMENT, "bytes_per_page must be 4096 (INT8) or 8192 (FP16)");
+    return 0;
+  }
+  if (total_pages > INT32_MAX) {
+    fail(PG_ERROR_UNSUPPORTED, "total_pages must fit in int32");
+    return 0;
+  }
+  std::vector<int32_t> indptr(static_cast<size_t>(batch_size) + 1);
+  const int64_t per = total_pages / batch_size, extra = total_pages % batch_size;
+  indptr[0] = 0;
+  for (int32_t b = 0; b < batch_size; ++b)
+    indptr[b + 1] = static_cast<int32_t>(indptr[b] + per + (b < extra ? 1 : 0));
+  const std::vector<int32_t> last(static_cast<size_t>(batch_size), kPageSize);
+  std::vector<WorkItem> items;
+  std::vector<int32_t> item_ptr;
+  pg_decode_plan_t p{};
+  const int32_t rc = build_plan(indptr.data(), last.data(), batch_size,
+                                bytes_per_page == 4096 ? PG_KV_INT8 : PG_KV_FP16, nullptr, nullptr,
+                                kGqa * num_kv_heads, num_kv_heads, kHeadDim, kPageSize, 0, 0, 0,
+                                num_cus, items, item_ptr, p);
+  return rc == PG_OK ? p.split_pages : 0;
 }
 
 namespace pg {

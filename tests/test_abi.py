@@ -11,6 +11,7 @@ import subprocess
 from pathlib import Path
 
 import pytest
+import torch
 
 from pagegauge_amd import _capi
 
@@ -76,11 +77,27 @@ def test_workspace_bytes_closed_form():
     assert lib.pg_decode_workspace_bytes(0, 32, 1, 1) == 0
 
 
-def test_select_split_pages_fills_the_gpu():
+def test_select_split_pages_is_the_balanced_planners_choice():
+    from pagegauge_amd import decode
+
     lib = _capi.library()
-    assert lib.pg_select_split_pages(3072, 1, 8, 4096, 256) == 12
-    assert lib.pg_select_split_pages(100, 1, 8, 4096, 256) == 1
-    assert lib.pg_select_split_pages(10 ** 6, 1, 8, 4096, 256) == 64      # one lane per page
+    for pages, batch, nbytes, cus in ((3072, 1, 4096, 256), (100, 1, 4096, 256),
+                                      (8192, 8, 4096, 256), (8195, 8, 4096, 256),
+                                      (3072, 1, 8192, 256), (20480, 4, 4096, 128)):
+        per, extra = divmod(pages, batch)
+        indptr = [0]
+        for b in range(batch):
+            indptr.append(indptr[-1] + per + (b < extra))
+        plan, _, _ = decode.plan_work_items(
+            torch.tensor(indptr, dtype=torch.int32), torch.full((batch,), 16, dtype=torch.int32),
+            kv_data_type=torch.int8 if nbytes == 4096 else torch.float16, num_cus=cus)
+        assert lib.pg_select_split_pages(pages, batch, 8, nbytes, cus) == plan.split_pages
+    assert lib.pg_select_split_pages(3072, 1, 8, 4096, 256) == 28     # the B1/49K medium plan
+    # more pages than 4096 items of 64 pages: no plan
+    assert lib.pg_select_split_pages(10 ** 6, 1, 8, 4096, 256) == 0
+    assert "too many splits" in _capi.last_error()
+    assert lib.pg_select_split_pages(3072, 1, 8, 1000, 256) == 0
+    assert "bytes_per_page" in _capi.last_error()
 
 
 @pytest.mark.parametrize("kwargs,code,message", [
