@@ -10,6 +10,7 @@
 //   * a closed-form plan reproduces every item from the formula the kernel
 //     uses (tail items first, then the primary segment's);
 //   * rejected inputs leave a message in pg_last_error().
+// pg_select_split_pages is called on random uniform batches as well.
 // Usage: planner_fuzz <seed> <iterations>; prints
 // "ok <plans> <rejections> <closed-form plans>".
 #include <algorithm>
@@ -179,6 +180,17 @@ int main(int argc, char** argv) {
         check(items[i].segment == (t ? 1 : 0), "closed-form items keep their segment", iter);
       }
     }
+  }
+  // pg_select_split_pages over random uniform batches (and invalid arguments)
+  for (int iter = 0; iter < iterations / 4; ++iter) {
+    const int64_t pages = uniform(0, 9) == 0 ? uniform(-5, 0) : uniform(1, 400000);
+    const int batch = uniform(0, 9) == 0 ? uniform(-2, 0) : uniform(1, 600);
+    const int bytes = uniform(0, 9) == 0 ? uniform(0, 9000) : (uniform(0, 1) ? 4096 : 8192);
+    const int split = pg_select_split_pages(pages, batch, 8, bytes, uniform(0, 600));
+    const bool valid = pages > 0 && batch > 0 && (bytes == 4096 || bytes == 8192);
+    check(split >= 0 && split <= 64, "a split lies in 0..64", iter);
+    if (!valid) check(split == 0 && std::strlen(pg_last_error()) > 0, "bad arguments give 0", iter);
+    if (split == 0) check(std::strlen(pg_last_error()) > 0, "a zero split leaves a message", iter);
   }
   if (failures) return 1;
   std::printf("ok %d %d %d\n", plans, rejected, closed);
