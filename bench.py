@@ -320,7 +320,7 @@ def decode_config(torch, decode, w, scrub, samples: int):
                                   stream=s), samples, scrub)
     kernel_us = 1e3 * statistics.fmean(kernel)
     alg = w.algorithmic_bytes()
-    return {
+    res = {
         "lengths": w.lengths if len(w.lengths) <= 8 else len(w.lengths),
         "work_items": dec.num_work_items,
         "call_p50_us": round(1e3 * statistics.median(call), 3),
@@ -330,6 +330,21 @@ def decode_config(torch, decode, w, scrub, samples: int):
         "achieved_gbps": round(alg / (kernel_us * 1e-6) / 1e9, 1),
         "frac_of_peak": round(alg / (kernel_us * 1e-6) / 1e9 / HBM_PEAK_GBPS, 4),
     }
+    if w.fp16_k is not None:
+        # the same-way FP16 kernel over an FP16 copy of every page, timed alike
+        wrap16 = decode.BatchDecodeWithPagedKVCacheWrapper(
+            torch.empty(64 << 20, dtype=torch.uint8, device=w.query.device), "NHD")
+        wrap16.plan(w.fp16_indptr, w.fp16_indices, w.fp16_last_page_len, 32, 8, 128, 16,
+                    kv_data_type=torch.float16)
+        b16 = wrap16.bind(w.query, (w.fp16_k, w.fp16_v), out=torch.empty_like(w.query),
+                          lse=torch.empty_like(lse))
+        for _ in range(3):
+            scrub()
+            b16()
+        call16 = call_samples(torch, b16, samples, scrub)
+        res["fp16_same_way_call_p50_us"] = round(1e3 * statistics.median(call16), 3)
+        res["speedup_vs_fp16_same_way"] = round(statistics.median(call16) / statistics.median(call), 4)
+    return res
 
 
 # The reference paper's isolated-attention microbenchmark on RTX 5090
@@ -1296,8 +1311,9 @@ def main() -> int:
 
     other = None
     if not args.no_configs:
-        other = {"config1_b1_4k": decode_config(torch, decode, workloads.single_4k(args.seed, device=device),
-                                                scrub_clean, 30)}
+        other = {"config1_b1_4k": decode_config(
+            torch, decode, workloads.single_4k(args.seed, device=device, with_fp16_copy=True),
+            scrub_clean, 30)}
         # B1/49K through the heterogeneous one-table decode (same pages)
         out_h = torch.empty_like(w.query)
         het = heterogeneous_call(torch, decode, w, device, out_h)
@@ -1319,7 +1335,7 @@ def main() -> int:
         del wi
         ragged = {}
         for seed in workloads.VALIDATION_SEEDS[:3]:
-            wr = workloads.b8_ragged(seed, device=device)
+            wr = workloads.b8_ragged(seed, device=device, with_fp16_copy=True)
             ragged[str(seed)] = decode_config(torch, decode, wr, scrub_clean, 30)
             del wr
             torch.cuda.empty_cache()
