@@ -45,7 +45,9 @@ SOURCES = {
     "pg_error.cpp": [],
     "pg_plan.cpp": [],
     "pg_update.hip": ["-ffp-contract=off"],
-    "pg_decode.hip": [],
+    # the memory-clause scheduler keeps the partial kernel's page-group loads
+    # together: measured 1-3 % faster (B1/49K, 16K, B8 ragged), same bits
+    "pg_decode.hip": ["-mllvm", "-amdgpu-sched-strategy=max-memory-clause"],
     "pg_decoder.hip": [],
     "pg_probe.hip": [],
 }
