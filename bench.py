@@ -92,6 +92,12 @@ def parse_args() -> argparse.Namespace:
     return p.parse_args()
 
 
+def build_sources():
+    """Per-source extra compiler flags of the library (pagegauge_amd.build)."""
+    from pagegauge_amd import build
+    return build.SOURCES
+
+
 def summarize(values_ms):
     ordered = sorted(values_ms)
     n = len(ordered)
@@ -1432,6 +1438,7 @@ def main() -> int:
         "validation_seeds_b1_49k": seeds,
         "parity_vs_oracle": parity,
         "library_variant": args.library_variant,
+        "library_flags": {src: flags for src, flags in build_sources().items() if flags},
         "output_sha256": hashlib.sha256(gpu_out.tobytes() + gpu_lse.tobytes()).hexdigest(),
         "split_sweep": sweep or None,
         "other_configs": other,
