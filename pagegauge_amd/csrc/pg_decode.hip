@@ -1052,10 +1052,12 @@ extern "C" int32_t pg_decode_plan(const int32_t* host_indptr, const int32_t* hos
   std::vector<WorkItem> items;
   std::vector<int32_t> item_ptr;
   pg_decode_plan_t p{};
-  const int32_t rc = build_plan(host_indptr, host_last_page_len, batch_size, primary_kind,
-                                host_tail_indptr, host_tail_last_len, num_qo_heads, num_kv_heads,
-                                head_dim, page_size, split_pages, tail_split_pages,
-                                exact_tail_pages_hint, num_cus, items, item_ptr, p);
+  const int32_t rc = guarded([&]() -> int32_t {
+    return build_plan(host_indptr, host_last_page_len, batch_size, primary_kind,
+                      host_tail_indptr, host_tail_last_len, num_qo_heads, num_kv_heads, head_dim,
+                      page_size, split_pages, tail_split_pages, exact_tail_pages_hint, num_cus,
+                      items, item_ptr, p);
+  });
   if (rc != PG_OK) return rc;
   if (p.workspace_bytes > workspace_bytes)
     return fail(PG_ERROR_WORKSPACE, "decode workspace too small: need " +

@@ -5,6 +5,8 @@
 
 #include <stdint.h>
 
+#include <exception>
+#include <new>
 #include <string>
 
 #include "pagegauge_hip.h"
@@ -23,6 +25,20 @@ void clear_error();
 inline int32_t fail(int32_t code, const std::string& message) {
   set_error(message);
   return code;
+}
+
+// Runs ``body`` (returning a PG_* code) so that no C++ exception unwinds
+// through the C ABI: a host allocation failure (an absurd batch size, say)
+// becomes an error code with its message.
+template <typename Body>
+int32_t guarded(Body&& body) {
+  try {
+    return body();
+  } catch (const std::bad_alloc&) {
+    return fail(PG_ERROR_UNSUPPORTED, "out of host memory while planning");
+  } catch (const std::exception& e) {
+    return fail(PG_ERROR_INVALID_ARGUMENT, e.what());
+  }
 }
 
 }  // namespace pg

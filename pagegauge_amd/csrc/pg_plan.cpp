@@ -64,19 +64,21 @@ extern "C" int32_t pg_select_split_pages(int64_t total_pages, int32_t batch_size
     fail(PG_ERROR_UNSUPPORTED, "total_pages must fit in int32");
     return 0;
   }
-  std::vector<int32_t> indptr(static_cast<size_t>(batch_size) + 1);
-  const int64_t per = total_pages / batch_size, extra = total_pages % batch_size;
-  indptr[0] = 0;
-  for (int32_t b = 0; b < batch_size; ++b)
-    indptr[b + 1] = static_cast<int32_t>(indptr[b] + per + (b < extra ? 1 : 0));
-  const std::vector<int32_t> last(static_cast<size_t>(batch_size), kPageSize);
-  std::vector<WorkItem> items;
-  std::vector<int32_t> item_ptr;
   pg_decode_plan_t p{};
-  const int32_t rc = build_plan(indptr.data(), last.data(), batch_size,
-                                bytes_per_page == 4096 ? PG_KV_INT8 : PG_KV_FP16, nullptr, nullptr,
-                                kGqa * num_kv_heads, num_kv_heads, kHeadDim, kPageSize, 0, 0, 0,
-                                num_cus, items, item_ptr, p);
+  const int32_t rc = guarded([&]() -> int32_t {
+    std::vector<int32_t> indptr(static_cast<size_t>(batch_size) + 1);
+    const int64_t per = total_pages / batch_size, extra = total_pages % batch_size;
+    indptr[0] = 0;
+    for (int32_t b = 0; b < batch_size; ++b)
+      indptr[b + 1] = static_cast<int32_t>(indptr[b] + per + (b < extra ? 1 : 0));
+    const std::vector<int32_t> last(static_cast<size_t>(batch_size), kPageSize);
+    std::vector<WorkItem> items;
+    std::vector<int32_t> item_ptr;
+    return build_plan(indptr.data(), last.data(), batch_size,
+                      bytes_per_page == 4096 ? PG_KV_INT8 : PG_KV_FP16, nullptr, nullptr,
+                      kGqa * num_kv_heads, num_kv_heads, kHeadDim, kPageSize, 0, 0, 0, num_cus,
+                      items, item_ptr, p);
+  });
   return rc == PG_OK ? p.split_pages : 0;
 }
 
@@ -309,21 +311,25 @@ extern "C" int32_t pg_decode_plan_host(const int32_t* host_indptr,
                                        int64_t items_capacity, int32_t* item_ptr_out) {
   clear_error();
   if (!plan) return fail(PG_ERROR_INVALID_ARGUMENT, "null plan argument");
-  std::vector<WorkItem> items;
-  std::vector<int32_t> item_ptr;
-  pg_decode_plan_t p{};
-  const int32_t rc = build_plan(host_indptr, host_last_page_len, batch_size, primary_kind,
-                                host_tail_indptr, host_tail_last_len, num_qo_heads, num_kv_heads,
-                                head_dim, page_size, split_pages, tail_split_pages,
-                                exact_tail_pages_hint, num_cus, items, item_ptr, p);
-  if (rc != PG_OK) return rc;
-  *plan = p;
-  if (items_out) {
-    if (items_capacity < static_cast<int64_t>(items.size()))
-      return fail(PG_ERROR_INVALID_ARGUMENT, "work-item buffer too small: need " +
-                                                 std::to_string(items.size()) + " items");
-    if (!items.empty()) std::memcpy(items_out, items.data(), items.size() * sizeof(WorkItem));
-  }
-  if (item_ptr_out) std::memcpy(item_ptr_out, item_ptr.data(), item_ptr.size() * sizeof(int32_t));
-  return PG_OK;
+  return guarded([&]() -> int32_t {
+    std::vector<WorkItem> items;
+    std::vector<int32_t> item_ptr;
+    pg_decode_plan_t p{};
+    const int32_t rc = build_plan(host_indptr, host_last_page_len, batch_size, primary_kind,
+                                  host_tail_indptr, host_tail_last_len, num_qo_heads,
+                                  num_kv_heads, head_dim, page_size, split_pages,
+                                  tail_split_pages, exact_tail_pages_hint, num_cus, items,
+                                  item_ptr, p);
+    if (rc != PG_OK) return rc;
+    *plan = p;
+    if (items_out) {
+      if (items_capacity < static_cast<int64_t>(items.size()))
+        return fail(PG_ERROR_INVALID_ARGUMENT, "work-item buffer too small: need " +
+                                                   std::to_string(items.size()) + " items");
+      if (!items.empty()) std::memcpy(items_out, items.data(), items.size() * sizeof(WorkItem));
+    }
+    if (item_ptr_out)
+      std::memcpy(item_ptr_out, item_ptr.data(), item_ptr.size() * sizeof(int32_t));
+    return PG_OK;
+  });
 }
