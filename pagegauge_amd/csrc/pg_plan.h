@@ -32,7 +32,7 @@ constexpr double kMediumMaxPagesPerCu = PG_MEDIUM_MAX_PAGES_PER_CU;
 
 struct WorkItem {
   int32_t request;
-  int32_t kind;        // PG_KV_INT8 or PG_KV_FP16
+  int32_t kind;        // PG_KV_INT8, PG_KV_FP16 or PG_KV_HETEROGENEOUS
   int32_t segment;     // 0 primary, 1 tail
   int32_t page_begin;  // absolute index into the segment's page-index array
   int32_t page_end;    // exclusive
@@ -47,8 +47,7 @@ static_assert(sizeof(WorkItem) == 48, "work item layout");
 // Work item ``i`` of a one-request plan: the FP16 tail segment's items
 // first, then the primary segment's; segment pages [base, base + n) in c
 // nearly equal chunks (the first n % c one page longer), as the planner
-// cuts them.
-// (constexpr: callable from the partial kernel as well as the planner)
+// cuts them.  constexpr, so the partial kernel calls it as well.
 constexpr WorkItem closed_form_item(int i, int items, int tail_items, int tail_begin,
                                     int tail_pages, int primary_begin, int primary_pages,
                                     int primary_kind) {
