@@ -36,6 +36,35 @@ def oracle_decode(w, with_tail: bool = True, with_center: bool = True):
                          k_scale=cpu(w.k_scale), v_scale=cpu(w.v_scale), **kw)
 
 
+def fp16_parity(out, ref16, ref64, tol: float = 2e-3) -> dict:
+    """The 2e-3 bar for an FP16 attention output against the float64 oracle.
+
+    ``ref16`` is the oracle rounded to FP16 (what the reference's own path
+    returns), ``ref64`` the unrounded oracle.  An element passes when it is
+    within ``tol`` of ``ref16``, or when it is the FP16 rounding of some value
+    within ``tol`` of ``ref64`` (the distance from ``ref64`` to the interval
+    of reals that round to it is at most ``tol``).  The second clause admits
+    the other neighbour of a value that lies on a rounding midpoint: past
+    |x| = 4 one FP16 ulp is already 3.9e-3, so a kernel exact to 1e-7 could
+    otherwise fail by the rounding alone.  Returns the worst difference to
+    ``ref16``, how many elements passed only by the second clause, and the
+    worst distance to the rounding interval; ``ok`` is whether all passed."""
+    got16 = (cpu(out) if not isinstance(out, np.ndarray) else out).astype(np.float16)
+    got = got16.astype(np.float64)
+    r16 = np.asarray(ref16).astype(np.float64)
+    r64 = np.asarray(ref64).astype(np.float64)
+    up = np.nextafter(got16, np.float16(np.inf)).astype(np.float64)
+    down = np.nextafter(got16, np.float16(-np.inf)).astype(np.float64)
+    # the reals that round to ``got``: half-way to each FP16 neighbour
+    gap = np.where(r64 >= got, (r64 - got) - 0.5 * (up - got), (got - r64) - 0.5 * (got - down))
+    d16 = np.abs(got - r16)
+    near = d16 <= tol
+    rounding = ~near & (gap <= tol)
+    return {"max_fp16_diff": float(d16.max()), "boundary_flips": int(rounding.sum()),
+            "max_interval_gap": float(np.maximum(gap, 0.0).max()),
+            "ok": bool((near | rounding).all())}
+
+
 def max_abs(a, b) -> float:
     a = cpu(a) if not isinstance(a, np.ndarray) else a
     b = cpu(b) if not isinstance(b, np.ndarray) else b
