@@ -37,6 +37,7 @@ import hashlib
 import json
 import math
 import os
+import random
 import statistics
 import sys
 import time
@@ -1346,6 +1347,16 @@ def main() -> int:
             del wr
             torch.cuda.empty_cache()
         other["config3_b8_ragged"] = ragged
+        # a serving-sized batch: 256 requests of 16-240 INT8 pages (U, seeded)
+        # behind full 16-page rings, in one shuffled pool
+        rng = random.Random(20261210)
+        ws_lengths = [16 * (16 + rng.randint(16, 240)) for _ in range(256)]
+        wb = workloads.build_decode_workload(ws_lengths, 20261210, device=device,
+                                             with_fp16_copy=True)
+        other["serving_b256"] = decode_config(torch, decode, wb, scrub_clean, 20)
+        other["serving_b256"]["total_tokens"] = sum(ws_lengths)
+        del wb
+        torch.cuda.empty_cache()
         other["config4_update"] = update_config4(torch, device, 50)
         other["exact_tail_merge_center"] = exact_tail_merge_line(torch, device, scrub_clean)
         other["paper_b4_20k"] = paper_b4_20k(torch, decode, workloads, device, scrub_clean, 60)

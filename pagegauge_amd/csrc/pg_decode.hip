@@ -736,6 +736,17 @@ __device__ __forceinline__ void fma4(float4& acc, float w, const float4& v) {
   acc.w += w * v.w;
 }
 
+// The output of a combine: total * inv + center as one f32 fma, rounded to
+// f32 and then to FP16.  The empty asm makes the f32 value opaque, so that
+// the compiler cannot fold the FP16 rounding into a mixed-precision fma (one
+// rounding) in one combine kernel and not in the other: with it both return
+// the same bits for the same partials.
+__device__ __forceinline__ float combine_output(float total, float inv, float center) {
+  float o = __builtin_fmaf(total, inv, center);
+  asm volatile("" : "+v"(o));
+  return o;
+}
+
 // Shared memory of one combine unit (256 threads).
 struct CombineShared {
   float wave_max[kCombineThreads / kWave];
@@ -842,8 +853,10 @@ __device__ __forceinline__ void combine_unit(const CombineArgs& a, int row_head,
     const float l = sh.wave_l[0] + sh.wave_l[2];
     const bool empty = !(l > 0.0f);
     const float inv = empty ? 0.0f : 1.0f / l;
-    const float o4[4] = {total.x * inv + center4[0], total.y * inv + center4[1],
-                         total.z * inv + center4[2], total.w * inv + center4[3]};
+    const float o4[4] = {combine_output(total.x, inv, center4[0]),
+                         combine_output(total.y, inv, center4[1]),
+                         combine_output(total.z, inv, center4[2]),
+                         combine_output(total.w, inv, center4[3])};
     const int d = 32 * quarter + 4 * tid;
     uint16_t* out = a.out + static_cast<int64_t>(row_head) * kHeadDim + d;
     *reinterpret_cast<__half2*>(out) = __floats2half2_rn(o4[0], o4[1]);
@@ -857,6 +870,121 @@ __device__ __forceinline__ void combine_unit(const CombineArgs& a, int row_head,
 __global__ __launch_bounds__(kCombineThreads) void combine_kernel(CombineArgs a) {
   __shared__ CombineShared sh;
   combine_unit(a, blockIdx.x, blockIdx.y, threadIdx.x, true, sh);
+}
+
+// ---------------------------------------------------------------------------
+// Combine for plans of at most 32 items per request (large batches of short
+// requests): one wave per (request, query head) row, lane l holding dims 2l
+// and 2l + 1, four rows per workgroup, no LDS and no barrier.  The grid is a
+// quarter of the rows instead of four workgroups per row, so a batch of
+// thousands of rows fits in one wave of workgroups.
+//
+// The sums keep combine_unit's association, so both kernels return the same
+// bits for the same partials (and a request's output does not depend on
+// which kernel its batch selects): per item w*o (one rounding), the 16-row
+// tree of row16_sum over items 0-15 and over items 16-31 (at a DPP row's
+// lane 0: pairs 8 apart, then 4, 2 and 1 apart; IEEE addition commutes, so
+// the rotation direction does not matter), then their sum.
+// ---------------------------------------------------------------------------
+constexpr int kCombineRowsMaxItems = kCombineRows;   // 32
+// Below this many (request, query head) rows the four-workgroup kernel's
+// wider spread of loads wins over the row kernel's one wave per row
+// (measured, cold calls: B4 x 20K and B4 x 4K 1.7-1.8 us faster with four
+// workgroups per row, B8 0.4-1.3 us; from B16 the row kernel is 1.2-1.7 us
+// faster, B64 9 us, B256 38 us).
+#ifndef PG_COMBINE_ROWS_MIN_ROWS
+#define PG_COMBINE_ROWS_MIN_ROWS 512
+#endif
+constexpr int kCombineRowsMinRows = PG_COMBINE_ROWS_MIN_ROWS;
+constexpr int kCombineRowsPerBlock = kCombineThreads / kWave;
+
+// lane 0 of row16_sum over a[0..15]
+__device__ __forceinline__ float tree16(const float* a) {
+  float s1[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) s1[i] = a[i] + a[i + 8];
+  float s2[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) s2[i] = s1[i] + s1[i + 4];
+  return (s2[0] + s2[2]) + (s2[1] + s2[3]);
+}
+
+// kSlots (8, 16 or 32) >= the plan's largest item count: item rows past it
+// enter the trees as the +0 terms combine_unit's empty rows give.
+template <int kSlots>
+__global__ __launch_bounds__(kCombineThreads) void combine_rows_kernel(CombineArgs a, int rows) {
+  static_assert(kSlots <= kCombineRowsMaxItems, "one 32-row pass");
+  const int row_head = blockIdx.x * kCombineRowsPerBlock + static_cast<int>(threadIdx.x) / kWave;
+  if (row_head >= rows) return;   // whole waves
+  const int lane = threadIdx.x % kWave;
+  const int request = row_head / a.num_qo_heads;
+  const int qh = row_head % a.num_qo_heads;
+  const int64_t base = static_cast<int64_t>(row_head) * a.max_items;
+  const float* pm = a.partial_m + base;
+  const float* pl = a.partial_l + base;
+  const float* po = a.partial_o + base * kHeadDim + 2 * lane;
+
+  float center2[2] = {0.0f, 0.0f};
+  if (a.value_center != nullptr) {
+    const uint32_t bits = *reinterpret_cast<const uint32_t*>(
+        a.value_center + request * a.center_batch_stride + (qh / kGqa) * kHeadDim + 2 * lane);
+    center2[0] = half_bits_to_float(static_cast<uint16_t>(bits));
+    center2[1] = half_bits_to_float(static_cast<uint16_t>(bits >> 16));
+  }
+  const int count =
+      a.uniform_items > 0 ? a.uniform_items : a.item_ptr[request + 1] - a.item_ptr[request];
+  float2 ov[kSlots];
+  float mv[kSlots], lv[kSlots];
+#pragma unroll
+  for (int j = 0; j < kSlots; ++j) {
+    const bool planned = j < a.max_items;
+    ov[j] = planned ? *reinterpret_cast<const float2*>(po + static_cast<int64_t>(j) * kHeadDim)
+                    : make_float2(0.0f, 0.0f);
+    mv[j] = planned ? pm[j] : kNegInf;
+    lv[j] = planned ? pl[j] : 0.0f;
+  }
+  float m = kNegInf;
+#pragma unroll
+  for (int j = 0; j < kSlots; ++j) {
+    mv[j] = j < count ? mv[j] : kNegInf;
+    m = fmaxf(m, mv[j]);
+  }
+  float tx[kCombineRowsMaxItems], ty[kCombineRowsMaxItems], tl[kCombineRowsMaxItems];
+#pragma unroll
+  for (int j = 0; j < kCombineRowsMaxItems; ++j) {
+    float x = 0.0f, y = 0.0f, l = 0.0f;
+    if (j < kSlots && j < count) {
+      const float w = mv[j] != kNegInf ? __builtin_amdgcn_exp2f(mv[j] - m) : 0.0f;
+      x += w * ov[j].x;
+      y += w * ov[j].y;
+      l += w * lv[j];
+    }
+    tx[j] = x;
+    ty[j] = y;
+    tl[j] = l;
+  }
+  const float total_x = tree16(tx) + tree16(tx + 16);
+  const float total_y = tree16(ty) + tree16(ty + 16);
+  const float l = tree16(tl) + tree16(tl + 16);
+  const bool empty = !(l > 0.0f);
+  const float inv = empty ? 0.0f : 1.0f / l;
+  uint16_t* out = a.out + static_cast<int64_t>(row_head) * kHeadDim + 2 * lane;
+  *reinterpret_cast<__half2*>(out) = __floats2half2_rn(combine_output(total_x, inv, center2[0]),
+                                                       combine_output(total_y, inv, center2[1]));
+  if (lane == 0 && a.lse != nullptr) a.lse[row_head] = empty ? kNegInf : log2f(l) + m;
+}
+
+template <int kSlots>
+void launch_combine_rows(const CombineArgs& c, int rows, void* stream, void* stop_event) {
+  const dim3 grid((rows + kCombineRowsPerBlock - 1) / kCombineRowsPerBlock);
+  if (stop_event) {
+    hipExtLaunchKernelGGL(combine_rows_kernel<kSlots>, grid, dim3(kCombineThreads), 0,
+                          as_stream(stream), nullptr, static_cast<hipEvent_t>(stop_event), 0, c,
+                          rows);
+  } else {
+    hipLaunchKernelGGL(combine_rows_kernel<kSlots>, grid, dim3(kCombineThreads), 0,
+                       as_stream(stream), c, rows);
+  }
 }
 
 __device__ __forceinline__ void init_state(HeadState& st) {
@@ -1226,7 +1354,18 @@ int32_t launch_combine(const pg_decode_plan_t* plan, const void* value_center,
   // every request has the same number of items (always so for one request)
   c.uniform_items = plan->num_items == plan->batch_size * plan->max_items_per_request
                         ? plan->max_items_per_request : 0;
-  const dim3 grid(plan->batch_size * plan->num_qo_heads, kHeadDim / 32);
+  const int rows = plan->batch_size * plan->num_qo_heads;
+  if (c.max_items <= kCombineRowsMaxItems && rows >= kCombineRowsMinRows) {
+    if (c.max_items <= 8) {
+      launch_combine_rows<8>(c, rows, stream, stop_event);
+    } else if (c.max_items <= 16) {
+      launch_combine_rows<16>(c, rows, stream, stop_event);
+    } else {
+      launch_combine_rows<32>(c, rows, stream, stop_event);
+    }
+    return check_launch("decode_combine");
+  }
+  const dim3 grid(rows, kHeadDim / 32);
   if (stop_event) {
     hipExtLaunchKernelGGL(combine_kernel, grid, dim3(kCombineThreads), 0, as_stream(stream),
                           nullptr, static_cast<hipEvent_t>(stop_event), 0, c);
