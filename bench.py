@@ -1062,14 +1062,23 @@ def stream_probe(torch, w, bound, scrub, samples: int = 20, probes=STREAM_PROBES
     pages = int(w.old_indices.numel())
     best_cold = min(r["cold_us"] / r["pages"] for r in rows) * pages
     pattern_cold = rows[0]["cold_us"] / rows[0]["pages"] * pages
+    tail_pages = int(w.tail_indices.numel())
+    alg = w.algorithmic_bytes()
+    kernel_gbps = alg / kernel["cold"] / 1e3
     return {"metric": "load-only stream of the INT8 pages vs the decode partial kernel",
             "unit": "us", "probes": rows,
             "decode_partial_kernel_us": kernel,
             "int8_pages": pages,
+            "fp16_tail_pages": tail_pages,
             "kernel_over_own_pattern_cold": round(pattern_cold / kernel["cold"], 4),
             "kernel_over_best_probe_cold": round(best_cold / kernel["cold"], 4),
-            "note": "probe times scaled to the kernel's 3056 INT8 pages for the ratios; the kernel "
-                    "also streams 16 FP16 tail pages (1 MB) and computes"}
+            # the kernel's algorithmic bytes (INT8 and FP16 pages, scales, query,
+            # partials) per second against the probes' INT8 page rates
+            "kernel_cold_gbps": round(kernel_gbps, 1),
+            "kernel_gbps_over_own_pattern_cold": round(kernel_gbps / rows[0]["cold_gbps"], 4),
+            "note": f"probe times scaled to the kernel's {pages} INT8 pages for the time ratios; "
+                    f"the kernel also streams {tail_pages} FP16 tail pages "
+                    f"({tail_pages * 65536 / 1e6:.1f} MB) and computes"}
 
 
 # weight bytes of the config-5 decoder's projections (FP16 [rows, k])
@@ -1258,6 +1267,22 @@ def main() -> int:
                      lse=torch.empty(8, 32, dtype=torch.float32, device=device))
         result["config3_b8_ragged"] = stream_probe(torch, w8, b8, scrub_clean, probes=STREAM_PROBES_B8)
         del w8, d8, b8
+        # the serving-sized batch of the bench line (256 requests, the large plan)
+        rng = random.Random(20261210)
+        wb = workloads.build_decode_workload([16 * (16 + rng.randint(16, 240)) for _ in range(256)],
+                                             20261210, device=device)
+        db = decode.PageGaugeSegmentedDecode(torch.empty(128 << 20, dtype=torch.uint8, device=device))
+        db.plan(wb.old_indptr, wb.old_indices, wb.old_last_page_len, wb.tail_indptr,
+                wb.tail_indices, wb.tail_last_page_len)
+        bb = db.bind(wb.query, (wb.k_codes, wb.v_codes), wb.k_scale, wb.v_scale,
+                     (wb.tail_k, wb.tail_v), wb.value_center, out=torch.empty_like(wb.query),
+                     lse=torch.empty(256, 32, dtype=torch.float32, device=device))
+        n_int8 = int(wb.old_indptr[-1]) // 64 * 64     # whole items of every probe
+        result["serving_b256"] = stream_probe(torch, wb, bb, scrub_clean, probes=(
+            ("decode pattern, 32-page items, 8 heads per workgroup", n_int8, 32, 8, 2, 0),
+            ("decode pattern, 64-page items, 8 heads per workgroup", n_int8, 64, 8, 2, 0),
+            ("whole pages per workgroup, 16-page items", n_int8, 16, 8, 2, 2)))
+        del wb, db, bb
         result["decoder_weight_reads"] = weight_read_ceiling(torch, device, scrub_clean)
         print(json.dumps(result), flush=True)
         return 0

@@ -30,6 +30,12 @@ constexpr double kLargeBatchMinChunk = PG_LARGE_BATCH_MIN_CHUNK;  // weighted pa
 #endif
 constexpr double kMediumMaxPagesPerCu = PG_MEDIUM_MAX_PAGES_PER_CU;
 
+// KV heads (waves) per workgroup when a plan has more items than CUs.
+#ifndef PG_MULTI_ROUND_WAVES
+#define PG_MULTI_ROUND_WAVES 4
+#endif
+constexpr int kMultiRoundWaves = PG_MULTI_ROUND_WAVES;
+
 struct WorkItem {
   int32_t request;
   int32_t kind;        // PG_KV_INT8, PG_KV_FP16 or PG_KV_HETEROGENEOUS

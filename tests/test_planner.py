@@ -219,3 +219,13 @@ if given is not None:
         _check_cover(items, ptr.tolist(), old, tails)
         assert plan.max_items_per_request == max(int(ptr[b + 1] - ptr[b]) for b in range(len(old)))
         assert plan.waves_per_block in (1, 2, 4, 8) and 8 % plan.waves_per_block == 0
+
+
+@pytest.mark.parametrize("batch,pages,items", [(16, 1008, 272), (64, 496, 576), (128, 240, 640)])
+def test_multi_round_plans_use_four_wave_workgroups(batch, pages, items):
+    """More items than CUs: two 4-wave workgroups per CU instead of one
+    8-wave workgroup, so that one item's start-up overlaps another's stream;
+    plans of at most one item per CU keep their widths (above)."""
+    plan, _, _ = plan_work_items(_indptr([pages] * batch), [16] * batch,
+                                 _indptr([16] * batch), [16] * batch)
+    assert (plan.num_items, plan.waves_per_block) == (items, 4)
