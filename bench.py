@@ -37,7 +37,6 @@ import hashlib
 import json
 import math
 import os
-import random
 import statistics
 import sys
 import time
@@ -85,8 +84,9 @@ def parse_args() -> argparse.Namespace:
     p.add_argument("--library-variant", default=None,
                    help="time an alternative build (python -m pagegauge_amd.build --variant NAME) "
                         "instead of the product library; the JSON line names it")
-    p.add_argument("--workload", choices=("b1_49k", "config1"), default="b1_49k",
-                   help="workload of the --pmc-calls driver (config1: B=1, 4096 tokens)")
+    p.add_argument("--workload", choices=("b1_49k", "config1", "serving_b256"), default="b1_49k",
+                   help="workload of the --pmc-calls driver (config1: B=1, 4096 tokens; "
+                        "serving_b256: 256 ragged requests)")
     p.add_argument("--pmc-calls", type=int, default=0,
                    help="counter-collection driver for rocprofv3 --pmc: N cold decode calls, "
                         "then N plain 64 MiB copies of known size; prints one JSON line, no timing")
@@ -1206,6 +1206,8 @@ def main() -> int:
     t_setup = time.perf_counter()
     if args.pmc_calls and args.workload == "config1":
         w = workloads.single_4k(args.seed, device=device, with_fp16_copy=not args.no_fp16)
+    elif args.pmc_calls and args.workload == "serving_b256":
+        w = workloads.serving_b256(device=device, with_fp16_copy=not args.no_fp16)
     else:
         w = workloads.b1_49k(args.seed, device=device, with_fp16_copy=not args.no_fp16)
     torch.cuda.synchronize()
@@ -1268,9 +1270,7 @@ def main() -> int:
         result["config3_b8_ragged"] = stream_probe(torch, w8, b8, scrub_clean, probes=STREAM_PROBES_B8)
         del w8, d8, b8
         # the serving-sized batch of the bench line (256 requests, the large plan)
-        rng = random.Random(20261210)
-        wb = workloads.build_decode_workload([16 * (16 + rng.randint(16, 240)) for _ in range(256)],
-                                             20261210, device=device)
+        wb = workloads.serving_b256(device=device)
         db = decode.PageGaugeSegmentedDecode(torch.empty(128 << 20, dtype=torch.uint8, device=device))
         db.plan(wb.old_indptr, wb.old_indices, wb.old_last_page_len, wb.tail_indptr,
                 wb.tail_indices, wb.tail_last_page_len)
@@ -1374,12 +1374,9 @@ def main() -> int:
         other["config3_b8_ragged"] = ragged
         # a serving-sized batch: 256 requests of 16-240 INT8 pages (U, seeded)
         # behind full 16-page rings, in one shuffled pool
-        rng = random.Random(20261210)
-        ws_lengths = [16 * (16 + rng.randint(16, 240)) for _ in range(256)]
-        wb = workloads.build_decode_workload(ws_lengths, 20261210, device=device,
-                                             with_fp16_copy=True)
+        wb = workloads.serving_b256(device=device, with_fp16_copy=True)
         other["serving_b256"] = decode_config(torch, decode, wb, scrub_clean, 20)
-        other["serving_b256"]["total_tokens"] = sum(ws_lengths)
+        other["serving_b256"]["total_tokens"] = sum(wb.lengths)
         del wb
         torch.cuda.empty_cache()
         other["config4_update"] = update_config4(torch, device, 50)

@@ -18,10 +18,13 @@ Configurations (shapes of the reference's Mistral-7B layer: 32 query heads,
     K/V ~ N(0,1) with x8 on 4 of 128 channels (separately for K and V);
   * ``single_4k``: one request, 4096 tokens (3840 INT8 + 256 FP16);
   * ``b8_ragged``: 8 requests with lengths U[4096, 32768] (multiples of 16);
+  * ``serving_b256``: 256 requests of 16-240 INT8 pages behind full rings;
   * arbitrary lengths through ``build_decode_workload``.
 """
 
 from __future__ import annotations
+
+import random
 
 from dataclasses import dataclass, field
 from typing import Optional, Sequence
@@ -230,6 +233,20 @@ def b1_49k(seed: int = VALIDATION_SEEDS[0], device="cuda", **kw) -> DecodeWorklo
 
 def single_4k(seed: int = VALIDATION_SEEDS[0], device="cuda", **kw) -> DecodeWorkload:
     return build_decode_workload([4096], seed, device=device, **kw)
+
+
+SERVING_SEED = 20261210
+
+
+def serving_lengths(seed: int = SERVING_SEED, batch: int = 256) -> list[int]:
+    """A serving-sized decode batch: ``batch`` requests of 16-240 INT8 pages
+    (uniform, seeded) behind full 16-page FP16 rings."""
+    rng = random.Random(seed)
+    return [PAGE * (TAIL_TOKENS // PAGE + rng.randint(16, 240)) for _ in range(batch)]
+
+
+def serving_b256(seed: int = SERVING_SEED, device="cuda", **kw) -> DecodeWorkload:
+    return build_decode_workload(serving_lengths(seed), seed, device=device, **kw)
 
 
 def ragged_lengths(seed: int, batch: int = 8, low: int = 4096, high: int = 32768) -> list[int]:
