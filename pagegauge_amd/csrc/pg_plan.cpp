@@ -42,6 +42,18 @@ int waves_per_block_for(int hkv, int64_t items, int64_t num_cus) {
   return w;
 }
 
+void order_for_dispatch(std::vector<WorkItem>& items, int32_t primary_kind, int32_t num_cus) {
+  const int64_t cus = num_cus > 0 ? num_cus : 256;
+  if (static_cast<int64_t>(items.size()) <= cus) return;
+  auto weight = [primary_kind](const WorkItem& it) {
+    const int pages = it.page_end - it.page_begin;
+    return it.kind == PG_KV_FP16 && primary_kind == PG_KV_INT8 ? 2 * pages : pages;
+  };
+  std::stable_sort(items.begin(), items.end(), [&](const WorkItem& a, const WorkItem& b) {
+    return weight(a) > weight(b);
+  });
+}
+
 }  // namespace pg
 
 using namespace pg;

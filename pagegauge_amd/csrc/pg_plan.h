@@ -92,4 +92,12 @@ int32_t build_plan(const int32_t* host_indptr, const int32_t* host_last_page_len
                    std::vector<WorkItem>& items, std::vector<int32_t>& item_ptr,
                    pg_decode_plan_t& p);
 
+// Device dispatch order of a plan's items: with more items than CUs
+// (several rounds of workgroups), the heaviest items first (FP16 pages
+// weigh twice INT8 pages when the primary segment is INT8), so that the last
+// round holds the lightest ones.  Stable; an item's partial row comes from
+// its request and item_in_request, not from its position, so any order gives
+// the same results.  The host-visible work list stays in request order.
+void order_for_dispatch(std::vector<WorkItem>& items, int32_t primary_kind, int32_t num_cus);
+
 }  // namespace pg
