@@ -44,6 +44,8 @@ def _segmented(w, workspace, split=None, tail_split=None, center=True):
     ([4096], 1), ([4096], 3), ([4096], 4), ([4096], 5), ([4096], 240),
     ([272, 2048, 512], None),   # ragged, shortest with a single history page
     ([4096 + 16 * 7, 1024], 7),
+    ([8192], 1),                # 496 + 16 one-page items: a one-request plan in two rounds
+    ([8192 + 16 * 5, 2048], 1), # the same over two requests (work list in dispatch order)
 ])
 def test_segmented_decode_matches_oracle(cuda, workspace, lengths, split):
     from pagegauge_amd import workloads
