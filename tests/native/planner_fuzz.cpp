@@ -21,6 +21,7 @@
 #include <vector>
 
 #include "pagegauge_hip.h"
+#include "pg_plan.h"
 
 namespace {
 
@@ -180,6 +181,31 @@ int main(int argc, char** argv) {
         check(items[i].segment == (t ? 1 : 0), "closed-form items keep their segment", iter);
       }
     }
+    // the device dispatch order (pg_decode_plan): a permutation of the work
+    // list; past one item per CU heaviest first, otherwise request order
+    std::vector<pg::WorkItem> order(n_items);
+    if (n_items > 0) std::memcpy(order.data(), raw.data(), n_items * sizeof(pg::WorkItem));
+    const std::vector<pg::WorkItem> listed = order;
+    pg::order_for_dispatch(order, kind, cus);
+    auto weight = [&](const pg::WorkItem& it) {
+      return (it.page_end - it.page_begin) * (it.kind == PG_KV_FP16 && kind == PG_KV_INT8 ? 2 : 1);
+    };
+    if (n_items <= cus) {
+      check(n_items == 0 || std::memcmp(order.data(), listed.data(),
+                                        n_items * sizeof(pg::WorkItem)) == 0,
+            "one-round plans keep request order", iter);
+    } else {
+      for (int i = 1; i < n_items; ++i)
+        check(weight(order[i - 1]) >= weight(order[i]), "heaviest items first", iter);
+    }
+    auto by_request = [](const pg::WorkItem& a, const pg::WorkItem& b) {
+      return a.request != b.request ? a.request < b.request : a.item_in_request < b.item_in_request;
+    };
+    std::vector<pg::WorkItem> x = order, y = listed;
+    std::sort(x.begin(), x.end(), by_request);
+    std::sort(y.begin(), y.end(), by_request);
+    check(n_items == 0 || std::memcmp(x.data(), y.data(), n_items * sizeof(pg::WorkItem)) == 0,
+          "the dispatch order is a permutation of the work list", iter);
   }
   // pg_select_split_pages over random uniform batches (and invalid arguments)
   for (int iter = 0; iter < iterations / 4; ++iter) {
