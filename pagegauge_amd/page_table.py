@@ -1,102 +1,194 @@
-"""Page-table algebra of the PageGauge decoder harness.
+"""Page tables of the PageGauge decoder harness.
 
-Host-side integer logic that partitions a context into exact prefix (sink),
-optional static exact suffix, INT8 "old" pages and the FP16 tail ring, and
-writes the compact int32 tables the decode kernels read.  Same names,
-arguments and error messages as
-``scripts/benchmark_page_gauge_transformer.py:383-749``; pinned by the golden
-lists of ``tests/test_page_gauge_transformer.py:100-216`` of the reference.
-Tables are torch int32 tensors on any device (the writers copy in place so a
-captured decode graph keeps reading the same storage).
+A request's context is a run of 16-token logical pages.  Each page is served
+either from the INT8 code pool ("old" pages) or from the request's exact FP16
+storage.  The exact storage of one request is a fixed block of slots:
+
+    [ prefix (sink) slots | static-suffix slots | tail ring slots ]
+      S pages               A pages               E pages
+
+* the first S logical pages (the attention sink) keep slots 0..S-1;
+* the A pages just before ``initial_context_pages`` (the static suffix of
+  the prefill) keep slots S..S+A-1;
+* every other page that is exact at some point is one of the newest E pages
+  of the context and lives in ring slot ``S + A + page % E``.
+
+``ExactPageLayout`` holds (S, A, I, E) and answers every question the
+decoder asks: the slot of a page, the slot table of a whole capacity, the
+partition of a context of T pages into old and exact pages, and the order in
+which the exact pages are listed for the exact decode segment.  The public
+functions keep the names, arguments, messages and return keys of the
+reference harness's page-table helpers
+(``scripts/benchmark_page_gauge_transformer.py:383-749``), whose behaviour
+the golden lists of its tests pin (``tests/test_page_gauge_transformer.py:
+100-216, 785-870``).  Tables are torch int32 tensors on any device; the
+writers fill a caller-owned destination in place, so a captured decode graph
+keeps reading the same storage.
 """
 
 from __future__ import annotations
 
-from typing import Any, Optional
+from dataclasses import dataclass
+from typing import Any, Optional, Sequence
 
 import torch
 
 PAGE = 16
 
 
-def request_major_page_table(batch_size: int, logical_page_capacity: int,
-                             physical_pages_per_request: Optional[int] = None,
-                             device="cuda") -> torch.Tensor:
-    """[B, P] map of logical pages to request-major physical storage (:383-405).
-
-    With ``physical_pages_per_request`` < P the logical pages wrap (a ring).
-    """
-    if batch_size <= 0 or logical_page_capacity <= 0:
-        raise ValueError("batch size and page capacity must be positive")
-    per_request = logical_page_capacity if physical_pages_per_request is None else physical_pages_per_request
-    if per_request <= 0:
-        raise ValueError("physical pages per request must be positive")
-    logical = torch.arange(logical_page_capacity, dtype=torch.int32, device=device)
-    base = torch.arange(batch_size, dtype=torch.int32, device=device) * per_request
-    return base[:, None] + (logical % per_request)[None, :]
-
-
+# ---------------------------------------------------------------------------
+# Argument checks (the reference's conditions and messages)
+# ---------------------------------------------------------------------------
 def validate_exact_prefix_pages(exact_prefix_pages: int) -> int:
-    if not isinstance(exact_prefix_pages, int) or exact_prefix_pages < 0:
-        raise ValueError("exact prefix pages must be a nonnegative integer")
-    return int(exact_prefix_pages)
+    """Exact prefix (attention sink) page count: a nonnegative int."""
+    if isinstance(exact_prefix_pages, int) and exact_prefix_pages >= 0:
+        return int(exact_prefix_pages)
+    raise ValueError("exact prefix pages must be a nonnegative integer")
 
 
 def validate_exact_static_suffix_pages(exact_static_suffix_pages: int, *,
                                        exact_prefix_pages: int = 0,
                                        initial_context_pages: Optional[int] = None) -> int:
+    """Static-suffix page count.  A nonzero suffix needs a positive initial
+    context that keeps at least one INT8 page between prefix and suffix."""
     if not isinstance(exact_static_suffix_pages, int) or exact_static_suffix_pages < 0:
         raise ValueError("exact static suffix pages must be a nonnegative integer")
-    if exact_static_suffix_pages:
-        if initial_context_pages is None or initial_context_pages <= 0:
-            raise ValueError("an exact static suffix requires positive initial context pages")
-        if exact_prefix_pages + exact_static_suffix_pages >= initial_context_pages:
-            raise ValueError("fixed exact prefix and suffix must leave an initial old-cache page")
+    if exact_static_suffix_pages == 0:
+        return 0
+    if initial_context_pages is None or initial_context_pages <= 0:
+        raise ValueError("an exact static suffix requires positive initial context pages")
+    if initial_context_pages <= exact_prefix_pages + exact_static_suffix_pages:
+        raise ValueError("fixed exact prefix and suffix must leave an initial old-cache page")
     return int(exact_static_suffix_pages)
 
 
 def validate_exact_sink_pages(exact_sink_pages: int) -> int:
-    """Legacy S0/S1 validator (sink of 0 or 1 page)."""
-    if exact_sink_pages not in (0, 1):
-        raise ValueError("exact sink pages must be 0 or 1")
-    return int(exact_sink_pages)
+    """Sink of 0 or 1 page (the reference's older S0/S1 protocol)."""
+    if exact_sink_pages in (0, 1):
+        return int(exact_sink_pages)
+    raise ValueError("exact sink pages must be 0 or 1")
 
 
 def validate_exact_prefix_attention_path(exact_prefix_pages: int, tail_attention: str) -> int:
-    exact_prefix_pages = validate_exact_prefix_pages(exact_prefix_pages)
-    if exact_prefix_pages and tail_attention != "flashinfer_merge":
+    """An exact prefix is served by the segmented path only (the fused tail
+    kernel and the one-table heterogeneous decode assume a lone tail)."""
+    pages = validate_exact_prefix_pages(exact_prefix_pages)
+    if pages and tail_attention != "flashinfer_merge":
         raise ValueError("exact prefix pages require the segmented flashinfer_merge path")
-    return exact_prefix_pages
+    return pages
 
 
-def _suffix_begin(exact_static_suffix_pages: int, initial_context_pages: Optional[int]):
-    if not exact_static_suffix_pages:
-        return None
-    return int(initial_context_pages) - exact_static_suffix_pages
+# ---------------------------------------------------------------------------
+# The layout of one request's exact storage
+# ---------------------------------------------------------------------------
+@dataclass(frozen=True)
+class ExactPageLayout:
+    prefix: int                 # S: sink pages, slots [0, S)
+    suffix: int                 # A: static-suffix pages, slots [S, S + A)
+    initial: Optional[int]      # I: initial context pages (the suffix ends there)
+    tail: int                   # E: ring pages, slots [S + A, S + A + E)
+
+    @classmethod
+    def checked(cls, prefix: int, suffix: int, initial: Optional[int],
+                tail: int) -> "ExactPageLayout":
+        """Layout after the prefix and suffix checks; callers check ``tail``
+        with their own message."""
+        prefix = validate_exact_prefix_pages(prefix)
+        suffix = validate_exact_static_suffix_pages(suffix, exact_prefix_pages=prefix,
+                                                    initial_context_pages=initial)
+        return cls(prefix, suffix, None if initial is None else int(initial), tail)
+
+    @property
+    def fixed(self) -> int:
+        """Slots that never move: prefix + static suffix."""
+        return self.prefix + self.suffix
+
+    @property
+    def storage(self) -> int:
+        """Exact slots per request."""
+        return self.fixed + self.tail
+
+    @property
+    def suffix_pages(self) -> range:
+        """Logical pages of the static suffix, [I - A, I)."""
+        if not self.suffix:
+            return range(0)
+        return range(self.initial - self.suffix, self.initial)
+
+    def slot(self, page: int) -> int:
+        """Exact slot of logical page ``page`` within its request."""
+        if page < self.prefix:
+            return page
+        span = self.suffix_pages
+        if page in span:
+            return self.prefix + (page - span.start)
+        return self.fixed + page % self.tail
+
+    def slots(self, capacity: int, device) -> torch.Tensor:
+        """``slot`` of logical pages 0..capacity-1 as int32 [capacity]: the ring
+        formula everywhere, then the prefix and suffix spans overwritten."""
+        pages = torch.arange(capacity, dtype=torch.int32, device=device)
+        local = pages.remainder(self.tail) + self.fixed
+        head = min(self.prefix, capacity)
+        local[:head] = pages[:head]
+        span = self.suffix_pages
+        lo, hi = span.start, min(span.stop, capacity)
+        if lo < hi:
+            local[lo:hi] = pages[lo:hi] - span.start + self.prefix
+        return local
+
+    def old_pages(self, total: int) -> list[int]:
+        """INT8 pages of a context of ``total`` pages, increasing: the pages
+        between the prefix and the tail ring, less the static suffix."""
+        tail_begin = total - self.tail
+        span = self.suffix_pages
+        if not span:
+            return list(range(self.prefix, tail_begin))
+        return (list(range(self.prefix, min(span.start, tail_begin))) +
+                list(range(max(span.stop, self.prefix), tail_begin)))
+
+    def exact_order(self, tail_begin: int, total: int) -> list[int]:
+        """Logical pages of the exact segment in table order: prefix, static
+        suffix, then the tail pages [tail_begin, total) in time order (tail
+        pages still inside the suffix are listed once, with the suffix)."""
+        span = self.suffix_pages
+        return (list(range(self.prefix)) + list(span) +
+                [p for p in range(tail_begin, total) if p not in span])
+
+
+def _request_major(batch_size: int, stride: int, local: torch.Tensor) -> torch.Tensor:
+    """[B, P] table: request r's block starts at r * stride."""
+    base = torch.arange(batch_size, dtype=torch.int32, device=local.device) * stride
+    return base[:, None] + local[None, :]
+
+
+# ---------------------------------------------------------------------------
+# Logical -> physical maps
+# ---------------------------------------------------------------------------
+def request_major_page_table(batch_size: int, logical_page_capacity: int,
+                             physical_pages_per_request: Optional[int] = None,
+                             device="cuda") -> torch.Tensor:
+    """[B, P] map of logical pages to request-major physical pages
+    (``:383-405``).  With fewer physical pages than P the logical pages wrap
+    around the request's block (a ring)."""
+    if batch_size <= 0 or logical_page_capacity <= 0:
+        raise ValueError("batch size and page capacity must be positive")
+    block = logical_page_capacity if physical_pages_per_request is None else physical_pages_per_request
+    if block <= 0:
+        raise ValueError("physical pages per request must be positive")
+    local = torch.arange(logical_page_capacity, dtype=torch.int32, device=device).remainder(block)
+    return _request_major(batch_size, block, local)
 
 
 def exact_physical_page_index(request: int, logical_page: int, exact_tail_pages: int,
                               exact_sink_pages: int = 0, exact_static_suffix_pages: int = 0,
                               initial_context_pages: Optional[int] = None) -> int:
-    """Physical exact-ring slot of one logical page (:455-489).
-
-    Storage per request: [prefix slots][static suffix slots][tail ring].
-    """
-    exact_sink_pages = validate_exact_prefix_pages(exact_sink_pages)
-    exact_static_suffix_pages = validate_exact_static_suffix_pages(
-        exact_static_suffix_pages, exact_prefix_pages=exact_sink_pages,
-        initial_context_pages=initial_context_pages)
-    if request < 0 or logical_page < 0 or exact_tail_pages <= 0:
+    """Physical exact slot of one logical page (``:455-489``)."""
+    layout = ExactPageLayout.checked(exact_sink_pages, exact_static_suffix_pages,
+                                     initial_context_pages, exact_tail_pages)
+    if min(request, logical_page) < 0 or exact_tail_pages <= 0:
         raise ValueError("exact page mapping inputs must be non-negative with a tail")
-    fixed = exact_sink_pages + exact_static_suffix_pages
-    suffix_begin = _suffix_begin(exact_static_suffix_pages, initial_context_pages)
-    if logical_page < exact_sink_pages:
-        local = logical_page
-    elif suffix_begin is not None and suffix_begin <= logical_page < int(initial_context_pages):
-        local = exact_sink_pages + logical_page - suffix_begin
-    else:
-        local = fixed + logical_page % exact_tail_pages
-    return request * (fixed + exact_tail_pages) + local
+    return request * layout.storage + layout.slot(logical_page)
 
 
 def request_major_exact_page_table(batch_size: int, logical_page_capacity: int,
@@ -104,72 +196,80 @@ def request_major_exact_page_table(batch_size: int, logical_page_capacity: int,
                                    exact_static_suffix_pages: int = 0,
                                    initial_context_pages: Optional[int] = None,
                                    device="cuda") -> torch.Tensor:
-    """[B, P] exact-slot table for every logical page (:492-524)."""
-    exact_sink_pages = validate_exact_prefix_pages(exact_sink_pages)
-    exact_static_suffix_pages = validate_exact_static_suffix_pages(
-        exact_static_suffix_pages, exact_prefix_pages=exact_sink_pages,
-        initial_context_pages=initial_context_pages)
-    if batch_size <= 0 or logical_page_capacity <= 0 or exact_tail_pages <= 0:
+    """[B, P] exact slot of every logical page (``:492-524``)."""
+    layout = ExactPageLayout.checked(exact_sink_pages, exact_static_suffix_pages,
+                                     initial_context_pages, exact_tail_pages)
+    if min(batch_size, logical_page_capacity, exact_tail_pages) <= 0:
         raise ValueError("batch, logical capacity, and exact tail must be positive")
-    if exact_sink_pages >= logical_page_capacity:
+    if layout.prefix >= logical_page_capacity:
         raise ValueError("exact prefix must be smaller than logical page capacity")
-    logical = torch.arange(logical_page_capacity, dtype=torch.int32, device=device)
-    fixed = exact_sink_pages + exact_static_suffix_pages
-    local = fixed + logical % exact_tail_pages
-    if exact_sink_pages:
-        local = torch.where(logical < exact_sink_pages, logical, local)
-    suffix_begin = _suffix_begin(exact_static_suffix_pages, initial_context_pages)
-    if suffix_begin is not None:
-        in_suffix = (logical >= suffix_begin) & (logical < int(initial_context_pages))
-        local = torch.where(in_suffix, exact_sink_pages + logical - suffix_begin, local)
-    base = torch.arange(batch_size, dtype=torch.int32, device=device) * (fixed + exact_tail_pages)
-    return base[:, None] + local[None, :].to(torch.int32)
+    return _request_major(batch_size, layout.storage, layout.slots(logical_page_capacity, device))
 
 
+# ---------------------------------------------------------------------------
+# Partition of a context
+# ---------------------------------------------------------------------------
 def page_gauge_logical_partition(total_pages: int, exact_tail_pages: int, exact_sink_pages: int,
                                  last_page_len: int, exact_static_suffix_pages: int = 0,
                                  initial_context_pages: Optional[int] = None) -> dict[str, Any]:
-    """Exact-once prefix / static suffix / old / tail partition (:527-587)."""
-    exact_sink_pages = validate_exact_prefix_pages(exact_sink_pages)
-    exact_static_suffix_pages = validate_exact_static_suffix_pages(
-        exact_static_suffix_pages, exact_prefix_pages=exact_sink_pages,
-        initial_context_pages=initial_context_pages)
+    """Old / exact split of a context of ``total_pages`` pages whose last page
+    holds ``last_page_len`` tokens (``:527-587``).  Every page gets one class,
+    so the old and exact lists cover the context exactly once."""
+    layout = ExactPageLayout.checked(exact_sink_pages, exact_static_suffix_pages,
+                                     initial_context_pages, exact_tail_pages)
     if total_pages <= 0 or exact_tail_pages <= 0:
         raise ValueError("total and exact-tail page counts must be positive")
     if not 1 <= last_page_len <= PAGE:
         raise ValueError("last page length lies outside one page")
     tail_begin = total_pages - exact_tail_pages
-    if tail_begin <= exact_sink_pages:
+    if tail_begin <= layout.prefix:
         raise ValueError("context must contain at least one quantized old page")
-    prefix = tuple(range(exact_sink_pages))
-    suffix_begin = _suffix_begin(exact_static_suffix_pages, initial_context_pages)
-    suffix = tuple(range(suffix_begin, int(initial_context_pages))) if suffix_begin is not None else ()
-    tail = tuple(range(tail_begin, total_pages))
-    exact_set = set(prefix) | set(suffix) | set(tail)
-    old = tuple(p for p in range(total_pages) if p not in exact_set)
-    exact = tuple(p for p in range(total_pages) if p in exact_set)
-    union = old + exact
-    disjoint = len(set(union)) == len(union) and set(union) == set(range(total_pages))
-    context_tokens = (total_pages - 1) * PAGE + last_page_len
-    old_tokens = len(old) * PAGE
-    exact_tokens = context_tokens - old_tokens
-    if not disjoint or old_tokens + exact_tokens != context_tokens:
-        raise RuntimeError("PageGauge logical partition is not exact and disjoint")
+
+    is_old = bytearray(total_pages)
+    for page in layout.old_pages(total_pages):
+        is_old[page] = 1
+    old = tuple(p for p in range(total_pages) if is_old[p])
+    exact = tuple(p for p in range(total_pages) if not is_old[p])
+    tokens = (total_pages - 1) * PAGE + last_page_len
+    old_tokens = PAGE * len(old)
+    prefix = tuple(range(layout.prefix))
     return {
         "prefix_logical_pages": prefix,
         "sink_logical_pages": prefix,
-        "static_suffix_logical_pages": suffix,
+        "static_suffix_logical_pages": tuple(layout.suffix_pages),
         "old_logical_pages": old,
-        "tail_logical_pages": tail,
+        "tail_logical_pages": tuple(range(tail_begin, total_pages)),
         "exact_logical_pages": exact,
         "tail_logical_begin": tail_begin,
         "old_page_count": len(old),
         "exact_page_count": len(exact),
         "old_token_count": old_tokens,
-        "exact_token_count": exact_tokens,
-        "context_token_count": context_tokens,
-        "coverage_disjoint": disjoint,
+        "exact_token_count": tokens - old_tokens,
+        "context_token_count": tokens,
+        "coverage_disjoint": len(old) + len(exact) == total_pages,
     }
+
+
+# ---------------------------------------------------------------------------
+# Active tables (written in place)
+# ---------------------------------------------------------------------------
+def _check_table_pair(what: str, destination: torch.Tensor, source: torch.Tensor) -> None:
+    """dtype, rank and batch checks shared by the old and exact writers."""
+    if destination.dtype != torch.int32 or source.dtype != torch.int32:
+        raise ValueError(f"{what} page tables must use int32 indices")
+    if destination.dim() != 2 or source.dim() != 2:
+        raise ValueError(f"{what} page tables must have shape [B,P]")
+    if destination.shape[0] != source.shape[0]:
+        raise ValueError(f"{what} page-table batch sizes differ")
+
+
+def _gather_columns(destination: torch.Tensor, source: torch.Tensor,
+                    columns: Sequence[int]) -> torch.Tensor:
+    """destination[:, j] = source[:, columns[j]]; returns the filled view."""
+    index = torch.tensor(list(columns), dtype=torch.long, device=source.device)
+    view = destination[:, :len(columns)]
+    view.copy_(source.index_select(1, index))
+    return view
 
 
 def write_exact_prefix_tail_page_table(destination: torch.Tensor,
@@ -177,67 +277,43 @@ def write_exact_prefix_tail_page_table(destination: torch.Tensor,
                                        tail_logical_begin: int, total_page_count: int,
                                        exact_sink_pages: int, exact_static_suffix_pages: int = 0,
                                        initial_context_pages: Optional[int] = None) -> torch.Tensor:
-    """Prefix slots, static suffix, then the chronological tail (:590-647)."""
-    exact_sink_pages = validate_exact_prefix_pages(exact_sink_pages)
-    exact_static_suffix_pages = validate_exact_static_suffix_pages(
-        exact_static_suffix_pages, exact_prefix_pages=exact_sink_pages,
-        initial_context_pages=initial_context_pages)
-    if destination.dtype != torch.int32 or logical_to_exact_physical.dtype != torch.int32:
-        raise ValueError("exact page tables must use int32 indices")
-    if destination.dim() != 2 or logical_to_exact_physical.dim() != 2:
-        raise ValueError("exact page tables must have shape [B,P]")
-    if destination.shape[0] != logical_to_exact_physical.shape[0]:
-        raise ValueError("exact page-table batch sizes differ")
-    if not exact_sink_pages <= tail_logical_begin < total_page_count:
+    """Exact-segment table: prefix slots, static suffix, then the tail in time
+    order (``:590-647``)."""
+    layout = ExactPageLayout.checked(exact_sink_pages, exact_static_suffix_pages,
+                                     initial_context_pages, 0)
+    _check_table_pair("exact", destination, logical_to_exact_physical)
+    if not layout.prefix <= tail_logical_begin < total_page_count:
         raise ValueError("exact prefix and tail logical ranges overlap or are empty")
     if total_page_count > logical_to_exact_physical.shape[1]:
         raise ValueError("exact logical page table exceeds allocated capacity")
-    suffix_begin = _suffix_begin(exact_static_suffix_pages, initial_context_pages)
-    tail_pages = [p for p in range(tail_logical_begin, total_page_count)
-                  if not (suffix_begin is not None and suffix_begin <= p < int(initial_context_pages))]
-    active = exact_sink_pages + exact_static_suffix_pages + len(tail_pages)
-    if active > destination.shape[1]:
+    order = layout.exact_order(tail_logical_begin, total_page_count)
+    if len(order) > destination.shape[1]:
         raise ValueError("exact active table exceeds destination capacity")
-    if exact_sink_pages:
-        destination[:, :exact_sink_pages].copy_(logical_to_exact_physical[:, :exact_sink_pages])
-    cursor = exact_sink_pages
-    if suffix_begin is not None:
-        destination[:, cursor:cursor + exact_static_suffix_pages].copy_(
-            logical_to_exact_physical[:, suffix_begin:int(initial_context_pages)])
-        cursor += exact_static_suffix_pages
-    if tail_pages:
-        idx = torch.tensor(tail_pages, dtype=torch.long, device=logical_to_exact_physical.device)
-        destination[:, cursor:active].copy_(logical_to_exact_physical.index_select(1, idx))
-    return destination[:, :active]
+    return _gather_columns(destination, logical_to_exact_physical, order)
 
 
 def write_page_gauge_old_page_table(destination: torch.Tensor, logical_to_physical: torch.Tensor,
-                                    old_logical_pages: tuple[int, ...]) -> torch.Tensor:
-    """Write an exact-once old-page set in logical order (:650-674)."""
-    if destination.dtype != torch.int32 or logical_to_physical.dtype != torch.int32:
-        raise ValueError("old page tables must use int32 indices")
-    if destination.dim() != 2 or logical_to_physical.dim() != 2:
-        raise ValueError("old page tables must have shape [B,P]")
-    if destination.shape[0] != logical_to_physical.shape[0]:
-        raise ValueError("old page-table batch sizes differ")
-    if not old_logical_pages:
+                                    old_logical_pages: Sequence[int]) -> torch.Tensor:
+    """INT8-segment table for a set of old pages, in logical order (``:650-674``)."""
+    _check_table_pair("old", destination, logical_to_physical)
+    pages = tuple(old_logical_pages)
+    if not pages:
         raise ValueError("old page set cannot be empty")
-    if tuple(sorted(set(old_logical_pages))) != tuple(old_logical_pages):
+    if any(b <= a for a, b in zip(pages, pages[1:])):
         raise ValueError("old logical pages must be unique and increasing")
-    if old_logical_pages[-1] >= logical_to_physical.shape[1]:
+    if pages[-1] >= logical_to_physical.shape[1]:
         raise ValueError("old logical page exceeds allocated capacity")
-    if len(old_logical_pages) > destination.shape[1]:
+    if len(pages) > destination.shape[1]:
         raise ValueError("old page set exceeds destination capacity")
-    idx = torch.tensor(old_logical_pages, dtype=torch.long, device=logical_to_physical.device)
-    destination[:, :len(old_logical_pages)].copy_(logical_to_physical.index_select(1, idx))
-    return destination[:, :len(old_logical_pages)]
+    return _gather_columns(destination, logical_to_physical, pages)
 
 
 def write_exact_sink_tail_page_table(destination: torch.Tensor,
                                      logical_to_exact_physical: torch.Tensor,
                                      tail_logical_begin: int, total_page_count: int,
                                      exact_sink_pages: int) -> torch.Tensor:
-    """Legacy name of ``write_exact_prefix_tail_page_table`` (:677-692)."""
+    """Older name of ``write_exact_prefix_tail_page_table`` without a suffix
+    (``:677-692``)."""
     return write_exact_prefix_tail_page_table(destination, logical_to_exact_physical,
                                               tail_logical_begin, total_page_count,
                                               exact_sink_pages)
@@ -246,24 +322,24 @@ def write_exact_sink_tail_page_table(destination: torch.Tensor,
 def write_heterogeneous_page_table(destination: torch.Tensor, old_pages: torch.Tensor,
                                    exact_ring_pages: torch.Tensor, old_page_count: int,
                                    total_page_count: int) -> torch.Tensor:
-    """One table over INT8 storage (< old_page_count) then the exact ring (:695-727)."""
+    """One table per request for the heterogeneous decode (``:695-727``):
+    columns below ``old_page_count`` come from the INT8 map, the rest up to
+    ``total_page_count`` from the exact-ring map."""
     if destination.dtype != torch.int32:
         raise ValueError("heterogeneous page table must use int32 indices")
-    if (destination.dim() != 2 or old_pages.shape != destination.shape
-            or exact_ring_pages.shape != destination.shape):
+    if destination.dim() != 2 or not (old_pages.shape == exact_ring_pages.shape == destination.shape):
         raise ValueError("heterogeneous page tables must have matching [B,P] shapes")
     if not 0 <= old_page_count <= total_page_count <= destination.shape[1]:
         raise ValueError("heterogeneous page counts lie outside table capacity")
-    if old_page_count:
-        destination[:, :old_page_count].copy_(old_pages[:, :old_page_count])
-    if old_page_count < total_page_count:
-        destination[:, old_page_count:total_page_count].copy_(
-            exact_ring_pages[:, old_page_count:total_page_count])
+    for source, lo, hi in ((old_pages, 0, old_page_count),
+                           (exact_ring_pages, old_page_count, total_page_count)):
+        if lo < hi:
+            destination[:, lo:hi].copy_(source[:, lo:hi])
     return destination[:, :total_page_count]
 
 
 def flatten_page_table(table: torch.Tensor, pages_per_request) -> tuple[torch.Tensor, torch.Tensor]:
-    """[B, P] table + per-request page counts -> (indptr [B+1], indices) int32."""
+    """[B, P] table + per-request page counts -> CSR (indptr [B+1], indices) int32."""
     counts = [int(c) for c in pages_per_request]
     if len(counts) != table.shape[0]:
         raise ValueError("one page count per request is required")

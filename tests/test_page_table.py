@@ -1,8 +1,10 @@
 """Page-table algebra against the reference tests' golden lists (CPU).
 
-Golden values come from tests/test_page_gauge_transformer.py:100-216 and
-tests/test_flashinfer_page_affine_int8.py:50-57 of the reference; the
-exact-once partition invariants are checked over a sweep of shapes.
+Golden values come from tests/test_page_gauge_transformer.py:100-216,
+:377-427 and :785-870 and tests/test_flashinfer_page_affine_int8.py:50-57 of
+the reference; the partition, slot table and exact-table order are also
+checked against a page-by-page definition of the page classes over a sweep
+of shapes (a static suffix before, inside and behind the tail ring).
 """
 
 from __future__ import annotations
@@ -146,3 +148,157 @@ def test_old_page_table_writer_rejects_unsorted_sets():
     assert active.tolist() == [[1, 2, 4]]
     with pytest.raises(ValueError, match="unique and increasing"):
         pt.write_page_gauge_old_page_table(destination, full, (2, 1))
+
+
+def test_fixed_suffix_mapping_and_partition_are_exact_once():
+    """tests/test_page_gauge_transformer.py:785-824 of the reference."""
+    prefix, suffix, tail, initial = 4, 64, 48, 1280
+    storage = prefix + suffix + tail
+    assert pt.exact_physical_page_index(0, 0, tail, prefix, suffix, initial) == 0
+    assert pt.exact_physical_page_index(0, initial - suffix, tail, prefix, suffix, initial) == prefix
+    assert pt.exact_physical_page_index(0, initial - 1, tail, prefix, suffix,
+                                        initial) == prefix + suffix - 1
+    generated = initial
+    assert pt.exact_physical_page_index(0, generated, tail, prefix, suffix,
+                                        initial) == prefix + suffix + generated % tail
+    assert pt.exact_physical_page_index(1, generated, tail, prefix, suffix,
+                                        initial) == storage + prefix + suffix + generated % tail
+    first = pt.page_gauge_logical_partition(initial, tail, prefix, pt.PAGE, suffix, initial)
+    assert first["exact_page_count"] == prefix + suffix
+    assert first["old_logical_pages"] == tuple(range(prefix, initial - suffix))
+    assert first["coverage_disjoint"]
+    later = pt.page_gauge_logical_partition(initial + tail, tail, prefix, 13, suffix, initial)
+    assert later["exact_page_count"] == prefix + suffix + tail
+    assert set(later["old_logical_pages"]).isdisjoint(later["static_suffix_logical_pages"])
+    assert later["coverage_disjoint"]
+
+
+def test_fixed_suffix_active_tables_are_unique_and_keep_current_page_last():
+    """tests/test_page_gauge_transformer.py:827-870 of the reference."""
+    prefix, suffix, tail, initial = 4, 64, 48, 1280
+    logical = pt.request_major_exact_page_table(1, initial + 96, tail, prefix, suffix, initial,
+                                                device="cpu")
+    destination = torch.empty(1, prefix + suffix + tail, dtype=torch.int32)
+    first = pt.write_exact_prefix_tail_page_table(destination, logical, initial - tail, initial,
+                                                  prefix, suffix, initial)
+    assert first.shape[1] == prefix + suffix
+    assert len(set(first[0].tolist())) == prefix + suffix
+    nxt = pt.write_exact_prefix_tail_page_table(destination, logical, initial - tail + 1,
+                                                initial + 1, prefix, suffix, initial)
+    assert nxt.shape[1] == prefix + suffix + 1
+    assert len(set(nxt[0].tolist())) == prefix + suffix + 1
+    assert nxt[0, -1].item() == pt.exact_physical_page_index(0, initial, tail, prefix, suffix,
+                                                             initial)
+
+
+def test_decoder_style_fixed_suffix_tables():
+    """The tables of the reference's fixed-suffix decoder plan
+    (tests/test_page_gauge_transformer.py:377-427): capacity 10, tail 2,
+    prefix 1, suffix 2, initial context 8 pages, at 8 and 9 pages."""
+    full = pt.request_major_page_table(1, 10, device="cpu")
+    exact = pt.request_major_exact_page_table(1, 10, 2, 1, 2, 8, device="cpu")
+    old_dst = torch.empty(1, 10, dtype=torch.int32)
+    exact_dst = torch.empty(1, 5, dtype=torch.int32)
+    for pages, want_old, want_exact in ((8, [1, 2, 3, 4, 5], [0, 1, 2]),
+                                        (9, [1, 2, 3, 4, 5], [0, 1, 2, 3])):
+        part = pt.page_gauge_logical_partition(pages, 2, 1, 1 if pages == 9 else pt.PAGE, 2, 8)
+        old = pt.write_page_gauge_old_page_table(old_dst, full, part["old_logical_pages"])
+        ex = pt.write_exact_prefix_tail_page_table(exact_dst, exact, part["tail_logical_begin"],
+                                                   pages, 1, 2, 8)
+        assert old.tolist() == [want_old]
+        assert ex.tolist() == [want_exact]
+        assert part["old_page_count"] + part["exact_page_count"] == pages
+
+
+def _classify(page, total, tail, prefix, suffix, initial):
+    """Definition of the page classes, one page at a time."""
+    if page < prefix:
+        return "exact"
+    if suffix and initial - suffix <= page < initial:
+        return "exact"
+    if page >= total - tail:
+        return "exact"
+    return "old"
+
+
+@pytest.mark.parametrize("total,tail,prefix,suffix,initial", [
+    (20, 4, 1, 2, 12), (12, 4, 1, 2, 12), (13, 4, 1, 2, 12), (14, 4, 0, 3, 12),
+    (40, 3, 5, 0, None), (1300, 48, 4, 64, 1280), (1290, 48, 4, 64, 1280),
+    (30, 16, 2, 5, 25), (60, 16, 2, 5, 25)])
+def test_partition_tables_match_the_page_by_page_definition(total, tail, prefix, suffix, initial):
+    """Old/exact sets, slot table and exact-table order against the page-class
+    definition above, including a tail ring that still overlaps the suffix."""
+    part = pt.page_gauge_logical_partition(total, tail, prefix, 5, suffix, initial)
+    want_old = [p for p in range(total) if _classify(p, total, tail, prefix, suffix, initial) == "old"]
+    assert list(part["old_logical_pages"]) == want_old
+    assert list(part["exact_logical_pages"]) == [p for p in range(total) if p not in set(want_old)]
+    assert part["old_token_count"] == 16 * len(want_old)
+    assert part["exact_token_count"] == (total - 1) * 16 + 5 - 16 * len(want_old)
+    # slots: prefix fixed, suffix fixed after it, everything else on the ring
+    capacity = total + 7
+    table = pt.request_major_exact_page_table(3, capacity, tail, prefix, suffix, initial,
+                                              device="cpu")
+    storage = prefix + suffix + tail
+    for r in range(3):
+        for p in range(capacity):
+            if p < prefix:
+                want = p
+            elif suffix and initial - suffix <= p < initial:
+                want = prefix + p - (initial - suffix)
+            else:
+                want = prefix + suffix + p % tail
+            assert table[r, p].item() == r * storage + want
+            assert pt.exact_physical_page_index(r, p, tail, prefix, suffix, initial) == r * storage + want
+    # the exact table lists every exact page of the context once, on distinct slots
+    dst = torch.full((1, storage + 4), -1, dtype=torch.int32)
+    active = pt.write_exact_prefix_tail_page_table(dst, table[:1], part["tail_logical_begin"], total,
+                                                   prefix, suffix, initial)[0].tolist()
+    listed = list(range(prefix)) + (list(range(initial - suffix, initial)) if suffix else [])
+    listed += [p for p in range(total - tail, total) if p not in listed]
+    assert active == [table[0, p].item() for p in listed]
+    assert len(set(active)) == len(active)
+    exact_now = set(part["exact_logical_pages"])
+    assert exact_now <= set(listed)
+
+
+@pytest.mark.parametrize("call,match", [
+    (lambda: pt.exact_physical_page_index(-1, 0, 4), "non-negative with a tail"),
+    (lambda: pt.exact_physical_page_index(0, 0, 0), "non-negative with a tail"),
+    (lambda: pt.request_major_exact_page_table(1, 4, 2, 4, device="cpu"), "smaller than logical"),
+    (lambda: pt.request_major_exact_page_table(0, 4, 2, device="cpu"), "must be positive"),
+    (lambda: pt.request_major_page_table(1, 4, 0, device="cpu"), "physical pages per request"),
+    (lambda: pt.page_gauge_logical_partition(8, 2, 1, 0), "outside one page"),
+    (lambda: pt.page_gauge_logical_partition(8, 0, 1, 3), "must be positive"),
+    (lambda: pt.validate_exact_static_suffix_pages(2), "positive initial context"),
+    (lambda: pt.validate_exact_static_suffix_pages(-1), "nonnegative integer"),
+    (lambda: pt.validate_exact_sink_pages(2), "0 or 1"),
+])
+def test_page_table_messages(call, match):
+    with pytest.raises(ValueError, match=match):
+        call()
+
+
+def test_table_writers_reject_bad_tables():
+    good = torch.zeros(2, 8, dtype=torch.int32)
+    with pytest.raises(ValueError, match="exact page tables must use int32"):
+        pt.write_exact_prefix_tail_page_table(good.long(), good, 6, 8, 1)
+    with pytest.raises(ValueError, match="exact page tables must have shape"):
+        pt.write_exact_prefix_tail_page_table(good[0], good, 6, 8, 1)
+    with pytest.raises(ValueError, match="exact page-table batch sizes differ"):
+        pt.write_exact_prefix_tail_page_table(good[:1], good, 6, 8, 1)
+    with pytest.raises(ValueError, match="overlap or are empty"):
+        pt.write_exact_prefix_tail_page_table(good, good, 8, 8, 1)
+    with pytest.raises(ValueError, match="exceeds allocated capacity"):
+        pt.write_exact_prefix_tail_page_table(good, good, 6, 9, 1)
+    with pytest.raises(ValueError, match="exceeds destination capacity"):
+        pt.write_exact_prefix_tail_page_table(good[:, :2], good, 5, 8, 1)
+    with pytest.raises(ValueError, match="old page tables must use int32"):
+        pt.write_page_gauge_old_page_table(good, good.long(), (1,))
+    with pytest.raises(ValueError, match="old page set cannot be empty"):
+        pt.write_page_gauge_old_page_table(good, good, ())
+    with pytest.raises(ValueError, match="old logical page exceeds"):
+        pt.write_page_gauge_old_page_table(good, good, (1, 8))
+    with pytest.raises(ValueError, match="exceeds destination capacity"):
+        pt.write_page_gauge_old_page_table(good[:, :1], good, (1, 2))
+    with pytest.raises(ValueError, match="matching"):
+        pt.write_heterogeneous_page_table(good, good[:1], good, 1, 2)
