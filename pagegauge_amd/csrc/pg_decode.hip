@@ -257,10 +257,15 @@ __device__ __forceinline__ void int8_chunk(const DecodeArgs& a, const WorkItem& 
   }
   const int last_len = it.segment == 0 ? a.last_page_len[it.request] : a.tail_last_len[it.request];
 
-  // page scales (after the index arrives); the V scale's chunk maximum fixes
-  // the probability fixed point for the whole chunk
-  const float my_sk = lane < count ? half_bits_to_float(a.k_scale[static_cast<int64_t>(my_page) * hkv + kv]) : 0.0f;
-  const float my_sv = lane < count ? half_bits_to_float(a.v_scale[static_cast<int64_t>(my_page) * hkv + kv]) : 0.0f;
+  // Page scales of every lane's slot, loaded unconditionally: a slot past
+  // the chunk end holds the chunk's last page (the clamp above), whose scales
+  // no score reads and whose V scale is already in the chunk maximum.  Both
+  // loads leave together right after the index arrives and are converted
+  // only after the first group's K/V loads are issued (a conditional load
+  // compiles to a branch that waits for each load in turn, which put two
+  // more round trips in front of the first K/V load).
+  uint32_t sk_raw = a.k_scale[static_cast<int64_t>(my_page) * hkv + kv];
+  uint32_t sv_raw = a.v_scale[static_cast<int64_t>(my_page) * hkv + kv];
 
   // Loads: a uniform page base plus a fixed 32-bit lane offset.  Slots past
   // the chunk end re-read its last page: their scores are masked to -inf and
@@ -330,6 +335,12 @@ __device__ __forceinline__ void int8_chunk(const DecodeArgs& a, const WorkItem& 
   }
   // score scale for this lane's C row (head kg): 2^-q_exp(head kg) * sm_scale*log2e
   const float qscale = ldexpf(a.sm_scale_log2, -__shfl(q_exp, 4 * kg, kWave));
+  // the V scale's chunk maximum fixes the probability fixed point for the
+  // whole chunk
+  consume_point(sk_raw);
+  consume_point(sv_raw);
+  const float my_sk = half_bits_to_float(static_cast<uint16_t>(sk_raw));
+  const float my_sv = half_bits_to_float(static_cast<uint16_t>(sv_raw));
   float vmax = my_sv;
 #pragma unroll
   for (int off = 32; off > 0; off >>= 1) vmax = fmaxf(vmax, __shfl_xor(vmax, off, kWave));
@@ -584,7 +595,10 @@ __device__ __forceinline__ void fp16_pages(const DecodeArgs& a, int request, con
   const uint16_t* vp = vpages + kv * kHeadDim;
   const int count = end - begin;        // 1..64 (planner bound)
   const int last_slot = last_page - begin;
-  const int my_page = lane < count ? indices[begin + lane] : 0;
+  // Unconditional loads (a lane past the range re-reads its last page id;
+  // every lane reads its head's query row): a conditional load compiles to
+  // a branch that waits for it before the next load can leave.
+  const int my_page = indices[begin + min(lane, count - 1)];
 
   // Q operand: head h on row 4h; lanes of other rows hold zeros.
   v8h qa[4];
@@ -593,11 +607,8 @@ __device__ __forceinline__ void fp16_pages(const DecodeArgs& a, int request, con
                       static_cast<int64_t>(kv * kGqa + (m16 >> 2)) * kHeadDim;
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
-    if (q_row) {
-      qa[j] = *reinterpret_cast<const v8h*>(q + 32 * j + 8 * kg);
-    } else {
-      qa[j] = v8h{0, 0, 0, 0, 0, 0, 0, 0};
-    }
+    const v8h row = *reinterpret_cast<const v8h*>(q + 32 * j + 8 * kg);
+    qa[j] = q_row ? row : v8h{0, 0, 0, 0, 0, 0, 0, 0};
   }
   uint16_t* plds = reinterpret_cast<uint16_t*>(lds);   // [4 heads][2 parts][16 tokens] fp16
 
