@@ -84,6 +84,12 @@ def parse_args() -> argparse.Namespace:
     p.add_argument("--library-variant", default=None,
                    help="time an alternative build (python -m pagegauge_amd.build --variant NAME) "
                         "instead of the product library; the JSON line names it")
+    p.add_argument("--trace", default="",
+                   help="per-wave phase trace of the partial kernel from a trace build "
+                        "(python -m pagegauge_amd.build --variant trace, or "
+                        "trace_conditional_scales): the variant name; B1/49K, 16K and 4K, "
+                        "cold calls; prints one JSON line")
+    p.add_argument("--trace-calls", type=int, default=20)
     p.add_argument("--workload", choices=("b1_49k", "config1", "serving_b256"), default="b1_49k",
                    help="workload of the --pmc-calls driver (config1: B=1, 4096 tokens; "
                         "serving_b256: 256 ragged requests)")
@@ -781,6 +787,17 @@ def cpu_baseline(torch, w, device, calls: int = 20, configs: bool = True):
     return out
 
 
+def _probes():
+    """bench.py's probe library (libpagegauge_bench.so, include/pagegauge_bench.h)."""
+    from pagegauge_amd import _capi
+    return _capi.bench_library()
+
+
+def _probe_check(rc: int) -> None:
+    if rc != 0:
+        raise RuntimeError(f"probe: {_probes().pg_last_error().decode()} (code {rc})")
+
+
 def measure_peak(torch, device, w, scrub, samples: int = 10):
     """HBM read bandwidth on this box, beside the 8 TB/s specification, from
     the library's read probes (pg_probe_linear_read, pg_probe_page_walk):
@@ -791,9 +808,7 @@ def measure_peak(torch, device, w, scrub, samples: int = 10):
     favourable way to stream this cache).  Timed like the decode kernel:
     events stamped by the probe's own dispatch, mean over ``samples``, best
     of a few launch shapes."""
-    from pagegauge_amd import _capi
-
-    lib = _capi.library()
+    lib = _probes()
     stream = torch.cuda.current_stream().cuda_stream
     big = torch.ones((1 << 30) // 4, dtype=torch.int32, device=device)
     small = torch.ones(101316248 // 16 * 4, dtype=torch.int32, device=device)
@@ -805,15 +820,15 @@ def measure_peak(torch, device, w, scrub, samples: int = 10):
     torch.cuda.synchronize()
 
     def linear(t, blocks, ev=(None, None)):
-        _capi.check(lib.pg_probe_linear_read(t.data_ptr(), t.numel() * 4, sink.data_ptr(), blocks,
-                                             ev[0], ev[1], stream), "probe")
+        _probe_check(lib.pg_probe_linear_read(t.data_ptr(), t.numel() * 4, sink.data_ptr(),
+                                              sink.numel(), blocks, ev[0], ev[1], stream))
 
     pages = int(w.old_indices.numel())
 
     def walk(per_block, ev=(None, None)):
-        _capi.check(lib.pg_probe_page_walk(w.k_codes.data_ptr(), w.v_codes.data_ptr(),
-                                           w.old_indices.data_ptr(), pages, per_block, 16384,
-                                           sink.data_ptr(), ev[0], ev[1], stream), "probe")
+        _probe_check(lib.pg_probe_page_walk(w.k_codes.data_ptr(), w.v_codes.data_ptr(),
+                                            w.old_indices.data_ptr(), pages, per_block, 16384,
+                                            sink.data_ptr(), sink.numel(), ev[0], ev[1], stream))
 
     def timed(fn, before=None):
         """Mean dispatch-stamped duration (s) of ``fn(events)``."""
@@ -1016,11 +1031,9 @@ def stream_probe(torch, w, bound, scrub, samples: int = 20, probes=STREAM_PROBES
     the clean scrub) and hot, beside the decode's partial kernel timed the
     same way in the same process: how close the kernel comes to the stream of
     its own pattern.  Mean of dispatch-stamped durations."""
-    from pagegauge_amd import _capi
-
-    lib = _capi.library()
+    lib = _probes()
     stream = torch.cuda.current_stream().cuda_stream
-    sink = torch.empty(4096, dtype=torch.int32, device=w.query.device)
+    sink = torch.empty(1 << 16, dtype=torch.int32, device=w.query.device)
     events = [[torch.cuda.Event(enable_timing=True) for _ in range(2)] for _ in range(samples)]
     for pair in events:
         for e in pair:
@@ -1042,9 +1055,9 @@ def stream_probe(torch, w, bound, scrub, samples: int = 20, probes=STREAM_PROBES
     rows = []
     for label, pages, per_item, heads, depth, mode in probes:
         def walk(start, stop, pages=pages, per_item=per_item, heads=heads, depth=depth, mode=mode):
-            _capi.check(lib.pg_probe_decode_walk(
+            _probe_check(lib.pg_probe_decode_walk(
                 w.k_codes.data_ptr(), w.v_codes.data_ptr(), w.old_indices.data_ptr(), pages,
-                per_item, heads, depth, mode, sink.data_ptr(), start, stop, stream), "probe")
+                per_item, heads, depth, mode, sink.data_ptr(), sink.numel(), start, stop, stream))
         cold, hot = timed(walk, scrub), timed(walk, None)
         nbytes = pages * 2 * 16384
         rows.append({"probe": label, "pages": pages, "pages_per_item": per_item,
@@ -1091,9 +1104,7 @@ def weight_read_ceiling(torch, device, scrub, samples: int = 10):
     projection's weight bytes (pg_probe_linear_read, best launch shape, mean
     of dispatch-stamped durations): the ceiling of the projection kernels,
     which read every weight byte once per step with the same loads."""
-    from pagegauge_amd import _capi
-
-    lib = _capi.library()
+    lib = _probes()
     stream = torch.cuda.current_stream().cuda_stream
     sink = torch.empty(1 << 16, dtype=torch.int32, device=device)
     events = [[torch.cuda.Event(enable_timing=True) for _ in range(2)] for _ in range(samples)]
@@ -1109,8 +1120,9 @@ def weight_read_ceiling(torch, device, scrub, samples: int = 10):
         for blocks in (512, 1024, 2048, 4096, 8192):
             for a, b in events:
                 scrub()
-                _capi.check(lib.pg_probe_linear_read(buf.data_ptr(), nbytes, sink.data_ptr(), blocks,
-                                                     a.cuda_event, b.cuda_event, stream), "probe")
+                _probe_check(lib.pg_probe_linear_read(buf.data_ptr(), nbytes, sink.data_ptr(),
+                                                      sink.numel(), blocks, a.cuda_event,
+                                                      b.cuda_event, stream))
             torch.cuda.synchronize()
             t = 1e3 * statistics.fmean(a.elapsed_time(b) for a, b in events)
             best = t if best is None else min(best, t)
@@ -1119,6 +1131,127 @@ def weight_read_ceiling(torch, device, scrub, samples: int = 10):
         del buf
     torch.cuda.empty_cache()
     return out
+
+
+# Lanes of a trace row (pg_decode.hip, PG_TRACE builds): s_memrealtime marks
+# at 100 MHz, then registers and notes.
+TRACE_START, TRACE_IDS, TRACE_ISSUED, TRACE_SCALES = 0, 1, 2, 3
+TRACE_K, TRACE_V, TRACE_DONE, TRACE_END = 4, 20, 36, 52
+TRACE_XCC, TRACE_HWID, TRACE_ITEM, TRACE_KIND, TRACE_PAGES = 53, 54, 55, 56, 57
+TRACE_TICK_US = 0.01
+
+
+def _trace_stats(values):
+    import numpy as np
+    v = np.asarray(values, dtype=np.float64)
+    if v.size == 0:
+        return None
+    q = np.percentile(v, [10, 50, 90])
+    return {"p10": round(float(q[0]), 2), "p50": round(float(q[1]), 2),
+            "p90": round(float(q[2]), 2), "max": round(float(v.max()), 2), "n": int(v.size)}
+
+
+def trace_summary(rows_per_call, kernel_us):
+    """Phase statistics (µs) of the per-wave trace rows of several calls.
+
+    Times are relative to the first wave start on the same XCD in the same
+    call: the s_memrealtime counters of different XCDs are not aligned (on
+    this part XCDs 0 and 1 read about 1.9 µs behind the others, more than the
+    kernel's own event duration allows as a real skew).  Per INT8
+    wave: page-id round trip (ids - start), first group's data (K of group
+    0 - its issue), and per group g: the wait for K (K[g] - done[g-1]), QK,
+    softmax and the wait for V (V[g] - K[g]), PV issue (done[g] - V[g])."""
+    import numpy as np
+    agg = {k: [] for k in ("start_at", "ids_rtt", "ids_at", "issued_at", "first_k_after_issue",
+                           "first_k_at", "k_wait", "qk_to_v", "pv", "group_span", "end_at",
+                           "end_at_fp16", "end_at_int8_last_group")}
+    by_xcc = {}
+    for rows in rows_per_call:
+        r = rows.astype(np.int64) & 0xFFFFFFFF
+        xcc = r[:, TRACE_XCC] & 0xF
+        t0 = np.zeros(len(r), dtype=np.int64)
+        for x in np.unique(xcc):
+            t0[xcc == x] = r[xcc == x, TRACE_START].min()
+        rel = lambda col: ((r[:, col] - t0) & 0xFFFFFFFF) * TRACE_TICK_US  # noqa: E731
+        kind = r[:, TRACE_KIND]
+        int8 = kind == 0
+        agg["start_at"] += list(rel(TRACE_START))
+        agg["ids_at"] += list(rel(TRACE_IDS))
+        agg["ids_rtt"] += list(rel(TRACE_IDS) - rel(TRACE_START))
+        agg["issued_at"] += list(rel(TRACE_ISSUED))
+        agg["first_k_after_issue"] += list((rel(TRACE_K) - rel(TRACE_ISSUED))[int8])
+        agg["first_k_at"] += list(rel(TRACE_K)[int8])
+        agg["end_at"] += list(rel(TRACE_END))
+        agg["end_at_fp16"] += list(rel(TRACE_END)[~int8])
+        pages = r[:, TRACE_PAGES]
+        groups = np.minimum((pages + 3) // 4, 16)
+        for w in np.nonzero(int8)[0]:
+            n = int(groups[w])
+            k = [rel(TRACE_K + g)[w] for g in range(n)]
+            v = [rel(TRACE_V + g)[w] for g in range(n)]
+            d = [rel(TRACE_DONE + g)[w] for g in range(n)]
+            for g in range(n):
+                agg["qk_to_v"].append(v[g] - k[g])
+                agg["pv"].append(d[g] - v[g])
+                if g:
+                    agg["k_wait"].append(k[g] - d[g - 1])
+                    agg["group_span"].append(d[g] - d[g - 1])
+            agg["end_at_int8_last_group"].append(d[n - 1])
+        for x in np.unique(xcc):
+            by_xcc.setdefault(int(x), []).extend(list(rel(TRACE_END)[xcc == x]))
+    out = {k: _trace_stats(v) for k, v in agg.items()}
+    out["end_at_p50_by_xcc"] = {x: round(float(np.median(v)), 2) for x, v in sorted(by_xcc.items())}
+    out["kernel_event_mean_us"] = round(float(np.mean(kernel_us)), 3)
+    out["waves_per_call"] = int(rows_per_call[0].shape[0])
+    return out
+
+
+def phase_trace(torch, decode, workloads, device, scrub, calls: int):
+    """Per-wave phase trace of the partial kernel (trace build loaded), cold
+    calls after the clean scrub, at B1/49K, 16K and 4K."""
+    from pagegauge_amd import _capi
+
+    lib = _capi.library()
+    if not hasattr(lib, "pg_trace_set_buffer"):
+        raise RuntimeError("--trace needs a trace build (python -m pagegauge_amd.build --variant trace)")
+    result = {}
+    cases = (("b1_49k", lambda: workloads.b1_49k(workloads.VALIDATION_SEEDS[0], device=device)),
+             ("b1_16k", lambda: workloads.build_decode_workload([16384 + 16], workloads.VALIDATION_SEEDS[0],
+                                                                device=device)),
+             ("config1_4k", lambda: workloads.single_4k(workloads.VALIDATION_SEEDS[0], device=device)))
+    for name, make in cases:
+        w = make()
+        dec = decode.PageGaugeSegmentedDecode(torch.empty(64 << 20, dtype=torch.uint8, device=device))
+        dec.plan(w.old_indptr, w.old_indices, w.old_last_page_len, w.tail_indptr, w.tail_indices,
+                 w.tail_last_page_len)
+        bound = dec.bind(w.query, (w.k_codes, w.v_codes), w.k_scale, w.v_scale, (w.tail_k, w.tail_v),
+                         w.value_center, out=torch.empty_like(w.query),
+                         lse=torch.empty(w.batch, 32, dtype=torch.float32, device=device))
+        waves = dec.num_work_items * 8
+        buf = torch.zeros(waves * 64, dtype=torch.int32, device=device)
+        _capi.check(lib.pg_trace_set_buffer(buf.data_ptr(), buf.numel() * 4), "trace")
+        for _ in range(3):
+            scrub()
+            bound()
+        rows, kernel = [], []
+        for _ in range(calls):
+            start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            start.record()
+            stop.record()
+            buf.zero_()
+            scrub()
+            bound.partial_timed(start.cuda_event, stop.cuda_event)
+            bound.combine()
+            torch.cuda.synchronize()
+            kernel.append(1e3 * start.elapsed_time(stop))
+            rows.append(buf.view(waves, 64).cpu().numpy().copy())
+        _capi.check(lib.pg_trace_set_buffer(None, 0), "trace")
+        result[name] = {"work_items": dec.num_work_items,
+                        "waves_per_block": int(dec._state.plan.waves_per_block),
+                        **trace_summary(rows, kernel)}
+        del w, dec, bound, buf
+        torch.cuda.empty_cache()
+    return result
 
 
 PILOT_SPLITS = (0, 8, 16, 28, 48, 64)
@@ -1184,8 +1317,14 @@ def main() -> int:
     import numpy as np
     import torch
 
+    if args.trace:
+        args.library_variant = args.trace
     if args.library_variant:
         from pagegauge_amd import _capi, build
+        if not build.variant_is_current(args.library_variant):
+            print(f"the {args.library_variant} build is missing or older than the sources: run "
+                  f"python -m pagegauge_amd.build --variant {args.library_variant}", file=sys.stderr)
+            return 2
         _capi.LIBRARY_PATH = build.variant_library(args.library_variant)
     from pagegauge_amd import decode, workloads
 
@@ -1196,6 +1335,13 @@ def main() -> int:
     torch.cuda.set_device(device)
     if args.decoder_only:
         print(json.dumps(decoder_config5(torch, device, args.decoder_repeats)), flush=True)
+        return 0
+    if args.trace:
+        buf = torch.ones((args.big_scrub_mib << 20) // 4, dtype=torch.int32, device=device)
+        sink = torch.empty((), dtype=torch.int32, device=device)
+        print(json.dumps({"trace_build": args.trace, **phase_trace(
+            torch, decode, workloads, device, lambda: torch.amax(buf, dim=0, out=sink),
+            args.trace_calls)}), flush=True)
         return 0
     if args.paper_only:
         buf = torch.ones((args.big_scrub_mib << 20) // 4, dtype=torch.int32, device=device)

@@ -531,40 +531,6 @@ int32_t pg_decoder_qkv_rope_append(const void* weight, int32_t k, const void* x,
 int32_t pg_argmax_f32(const float* x, int32_t rows, int32_t n, int64_t row_stride, int64_t* out,
                       void* stream);
 
-/* ------------------------------------------------------------------------
- * HBM read probes (measurement helpers; no counterpart in the reference,
- * which never measures its GPU's peak).  They give the read bandwidth this
- * device reaches, the figure BASELINE's roofline asks to re-measure beside
- * the specification.  sink: int32 [blocks] (written only under a condition
- * on the loaded data; its contents are meaningless).
- * ---------------------------------------------------------------------- */
-
-/* Grid-stride read of ``bytes`` contiguous bytes (16-byte aligned multiple
- * of 16), 16 B per lane per load, ``blocks`` workgroups of 256 threads.
- * With start_event / stop_event (hipEvent_t, may be NULL) the dispatch
- * stamps its own begin and end. */
-int32_t pg_probe_linear_read(const void* src, int64_t bytes, int32_t* sink, int32_t blocks,
-                             void* start_event, void* stop_event, void* stream);
-/* Reads pages indices[0..pages) of two page pools, each page as one
- * contiguous block of ``page_bytes`` K bytes and ``page_bytes`` V bytes,
- * ``pages_per_block`` pages per 256-thread workgroup. */
-int32_t pg_probe_page_walk(const void* k_pages, const void* v_pages, const int32_t* indices,
-                           int32_t pages, int32_t pages_per_block, int32_t page_bytes,
-                           int32_t* sink, void* start_event, void* stop_event, void* stream);
-/* Reads pages indices[0..pages) the way the INT8 decode kernel does, loads
- * only: work items of ``pages_per_item`` consecutive entries (4..64, a
- * multiple of 4, dividing ``pages``), one wave per KV head (8 KV heads of
- * 128 codes, 16 KiB pages), ``heads_per_block`` (4 or 8) waves per
- * workgroup, 4-page groups with ``depth`` (1 or 2) groups in flight per wave.
- * ``mode`` 0 = the decode kernel's lane pattern, 1 = whole 128-byte head
- * rows per lane group, 2 = whole pages as contiguous 1 KiB per instruction
- * (heads_per_block 8).  Gives the stream rate of the decode's own access
- * pattern, to set the decode kernel against. */
-int32_t pg_probe_decode_walk(const void* k_pages, const void* v_pages, const int32_t* indices,
-                             int32_t pages, int32_t pages_per_item, int32_t heads_per_block,
-                             int32_t depth, int32_t mode, int32_t* sink, void* start_event,
-                             void* stop_event, void* stream);
-
 #ifdef __cplusplus
 }
 #endif

@@ -114,30 +114,48 @@ PROTOTYPES = {
     "pg_merge_state_in_place": (_i32, [_p, _p, _p, _p, _p, _i32, _i32, _i32, _p]),
     "pg_exact_tail_merge_center": (_i32, [_p, _p, _p, _p, _p, _p, _p, _p, _i64, _i32, _i32, _i32,
                                           _i32, _f32, _p]),
-    "pg_probe_linear_read": (_i32, [_p, _i64, _p, _i32, _p, _p, _p]),
-    "pg_probe_page_walk": (_i32, [_p, _p, _p, _i32, _i32, _i32, _p, _p, _p, _p]),
-    "pg_probe_decode_walk": (_i32, [_p, _p, _p, _i32, _i32, _i32, _i32, _i32, _p, _p, _p, _p]),
+}
+
+# libpagegauge_bench.so (include/pagegauge_bench.h): bench.py's probes
+BENCH_LIBRARY_PATH = LIBRARY_PATH.with_name("libpagegauge_bench.so")
+BENCH_PROTOTYPES = {
+    "pg_last_error": (ctypes.c_char_p, []),
+    "pg_abi_version": (_i32, []),
+    "pg_probe_linear_read": (_i32, [_p, _i64, _p, _i64, _i32, _p, _p, _p]),
+    "pg_probe_page_walk": (_i32, [_p, _p, _p, _i32, _i32, _i32, _p, _i64, _p, _p, _p]),
+    "pg_probe_decode_walk": (_i32, [_p, _p, _p, _i32, _i32, _i32, _i32, _i32, _p, _i64, _p, _p,
+                                    _p]),
+}
+
+# exported by the trace build of the product library only
+TRACE_PROTOTYPES = {
+    "pg_trace_set_buffer": (_i32, [_p, _i64]),
 }
 
 _lock = threading.Lock()
 _library = None
+_bench_library = None
 
 
 class LibraryMissingError(RuntimeError):
     pass
 
 
-def load_library(path):
+def load_library(path, prototypes=None):
     """A ctypes handle of the library at ``path`` with every prototype set
     and its ABI checked (not cached; ``library()`` holds the product's).
     Alternative builds (``python -m pagegauge_amd.build --variant NAME``)
-    load beside the product this way."""
+    load beside the product this way; the trace build also binds
+    ``pg_trace_set_buffer``."""
     if not Path(path).exists():
         raise LibraryMissingError(
             f"{path} is missing: build it with `python -c "
             "'import __graft_entry__ as g; g.build()'` (hipcc, gfx950)")
     lib = ctypes.CDLL(str(path))
-    for name, (restype, argtypes) in PROTOTYPES.items():
+    table = dict(PROTOTYPES if prototypes is None else prototypes)
+    if prototypes is None and hasattr(lib, "pg_trace_set_buffer"):
+        table.update(TRACE_PROTOTYPES)
+    for name, (restype, argtypes) in table.items():
         fn = getattr(lib, name)
         fn.restype = restype
         fn.argtypes = argtypes
@@ -157,6 +175,17 @@ def library():
         if _library is None:
             _library = load_library(LIBRARY_PATH)
     return _library
+
+
+def bench_library():
+    """Load (once) and return bench.py's probe library (libpagegauge_bench.so)."""
+    global _bench_library
+    if _bench_library is not None:
+        return _bench_library
+    with _lock:
+        if _bench_library is None:
+            _bench_library = load_library(BENCH_LIBRARY_PATH, BENCH_PROTOTYPES)
+    return _bench_library
 
 
 def last_error() -> str:

@@ -71,6 +71,36 @@ constexpr int kLdsPerWave = 1024;       // INT8 P digits: [4 pages][4 heads][4 d
 constexpr int kCombineThreads = 256;
 constexpr float kNegInf = -__builtin_huge_valf();
 
+// Phase trace of the partial kernel (PG_TRACE builds only, an alternative
+// build for bench.py --trace; the product compiles none of it).  Each wave
+// records s_memrealtime (100 MHz) marks into the lanes of one register and
+// writes them as one 64-word row when it ends.  A mark placed after a load
+// reads a register that load fills, so it waits for the load as the
+// kernel's own consume points do.  Lanes of the row:
+#ifndef PG_TRACE
+#define PG_TRACE 0
+#endif
+constexpr int kTraceStart = 0;      // first instruction of the wave
+constexpr int kTraceIds = 1;        // page ids of the chunk arrived
+constexpr int kTraceIssued = 2;     // first group's K/V loads issued
+constexpr int kTraceScales = 3;     // page scales arrived
+constexpr int kTraceK = 4;          // + g: K codes of group g (FP16: page g) arrived, g < 16
+constexpr int kTraceV = 20;         // + g: V codes of INT8 group g arrived
+constexpr int kTraceDone = 36;      // + g: group g's PV products issued
+constexpr int kTraceEnd = 52;       // softmax state final, before the partial write
+constexpr int kTraceXcc = 53;       // XCC_ID hardware register
+constexpr int kTraceHwId = 54;      // HW_ID hardware register (CU, SIMD, wave slot)
+constexpr int kTraceItem = 55;      // (blockIdx.x << 8) | kv head
+constexpr int kTraceKind = 56;      // work item kind
+constexpr int kTracePages = 57;     // pages of the chunk
+constexpr int kTraceSlots = 16;     // traced groups (FP16 pages) per wave
+// Alternative build for the trace's before/after only: the page-scale loads
+// in the conditional form the kernel had before (each compiled to a branch
+// that waits for its load before the next one leaves).
+#ifndef PG_CONDITIONAL_SCALE_LOADS
+#define PG_CONDITIONAL_SCALE_LOADS 0
+#endif
+
 struct DecodeArgs {
   const uint16_t* query;
   int64_t query_batch_stride;
@@ -112,6 +142,9 @@ struct DecodeArgs {
   int8_t* finalize_v_codes;
   uint16_t* finalize_k_scale;
   uint16_t* finalize_v_scale;
+#if PG_TRACE
+  uint32_t* trace;    // [waves of the grid][64] words, or null
+#endif
 };
 
 // Per-lane softmax/output state of one KV head (4 query heads).
@@ -120,7 +153,43 @@ struct HeadState {
   float m;
   float l;
   float o[8];
+#if PG_TRACE
+  uint32_t trace;   // lane i: trace word i
+#endif
 };
+
+#if PG_TRACE
+__device__ __forceinline__ void trace_put(HeadState& st, int slot, uint32_t value) {
+  st.trace = static_cast<int>(threadIdx.x % kWave) == slot ? value : st.trace;
+}
+__device__ __forceinline__ void trace_mark(HeadState& st, int slot) {
+  uint64_t t;
+  asm volatile("s_memrealtime %0\n\ts_waitcnt lgkmcnt(0)" : "=s"(t) : : "memory");
+  trace_put(st, slot, static_cast<uint32_t>(t));
+}
+__device__ __forceinline__ void trace_mark_after(HeadState& st, int slot, uint32_t loaded) {
+  uint64_t t;
+  asm volatile("s_memrealtime %0\n\ts_waitcnt lgkmcnt(0)" : "=s"(t) : "v"(loaded) : "memory");
+  trace_put(st, slot, static_cast<uint32_t>(t));
+}
+__device__ __forceinline__ uint32_t trace_hwreg_xcc() {
+  uint32_t x;
+  asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID)" : "=s"(x));
+  return x;
+}
+__device__ __forceinline__ uint32_t trace_hwreg_id() {
+  uint32_t x;
+  asm volatile("s_getreg_b32 %0, hwreg(HW_REG_HW_ID)" : "=s"(x));
+  return x;
+}
+#define PG_TRACE_MARK(st, slot) trace_mark((st), (slot))
+#define PG_TRACE_AFTER(st, slot, loaded) trace_mark_after((st), (slot), static_cast<uint32_t>(loaded))
+#define PG_TRACE_PUT(st, slot, value) trace_put((st), (slot), static_cast<uint32_t>(value))
+#else
+#define PG_TRACE_MARK(st, slot) ((void)0)
+#define PG_TRACE_AFTER(st, slot, loaded) ((void)0)
+#define PG_TRACE_PUT(st, slot, value) ((void)0)
+#endif
 
 // 4x4 byte transpose: r[k] holds 4 dims of token k; returns c[j] holding
 // dim j of tokens 0..3.  v_perm_b32(hi, lo, sel) picks byte sel_i of the
@@ -264,8 +333,14 @@ __device__ __forceinline__ void int8_chunk(const DecodeArgs& a, const WorkItem& 
   // only after the first group's K/V loads are issued (a conditional load
   // compiles to a branch that waits for each load in turn, which put two
   // more round trips in front of the first K/V load).
+#if PG_CONDITIONAL_SCALE_LOADS
+  const float sk_early = lane < count ? half_bits_to_float(a.k_scale[static_cast<int64_t>(my_page) * hkv + kv]) : 0.0f;
+  const float sv_early = lane < count ? half_bits_to_float(a.v_scale[static_cast<int64_t>(my_page) * hkv + kv]) : 0.0f;
+  uint32_t sk_raw = 0u, sv_raw = 0u;
+#else
   uint32_t sk_raw = a.k_scale[static_cast<int64_t>(my_page) * hkv + kv];
   uint32_t sv_raw = a.v_scale[static_cast<int64_t>(my_page) * hkv + kv];
+#endif
 
   // Loads: a uniform page base plus a fixed 32-bit lane offset.  Slots past
   // the chunk end re-read its last page: their scores are masked to -inf and
@@ -293,7 +368,10 @@ __device__ __forceinline__ void int8_chunk(const DecodeArgs& a, const WorkItem& 
       for (int t = 0; t < 4; ++t)
         dst.v[4 * i + t] = *reinterpret_cast<const v2u*>(vp[i] + v_off + t * row_stride);
   };
+  PG_TRACE_AFTER(st, kTraceIds, my_page);
   issue(0, buf[0]);
+  PG_TRACE_MARK(st, kTraceIssued);
+  PG_TRACE_PUT(st, kTracePages, count);
 
   // ---- query digits (overlaps the first group's loads)
   float qmax = 0.0f;
@@ -339,8 +417,14 @@ __device__ __forceinline__ void int8_chunk(const DecodeArgs& a, const WorkItem& 
   // whole chunk
   consume_point(sk_raw);
   consume_point(sv_raw);
+  PG_TRACE_AFTER(st, kTraceScales, sv_raw);
+#if PG_CONDITIONAL_SCALE_LOADS
+  const float my_sk = sk_early;
+  const float my_sv = sv_early;
+#else
   const float my_sk = half_bits_to_float(static_cast<uint16_t>(sk_raw));
   const float my_sv = half_bits_to_float(static_cast<uint16_t>(sv_raw));
+#endif
   float vmax = my_sv;
 #pragma unroll
   for (int off = 32; off > 0; off >>= 1) vmax = fmaxf(vmax, __shfl_xor(vmax, off, kWave));
@@ -389,6 +473,7 @@ __device__ __forceinline__ void int8_chunk(const DecodeArgs& a, const WorkItem& 
       consume_point(cur.k[i][0]);
       consume_point(cur.k[i][1]);
     }
+    if (PG_TRACE && g < kTraceSlots) PG_TRACE_AFTER(st, kTraceK + g, cur.k[kGroupPages - 1][1][3]);
     // ---- QK: exact integer dot products
     float s[kGroupPages];
     float svu[kGroupPages];
@@ -460,6 +545,7 @@ __device__ __forceinline__ void int8_chunk(const DecodeArgs& a, const WorkItem& 
     // dword per output dim; n-block nb covers output dim 8*(lane%16) + nb
 #pragma unroll
     for (int i = 0; i < 16; ++i) consume_point(cur.v[i]);
+    if (PG_TRACE && g < kTraceSlots) PG_TRACE_AFTER(st, kTraceV + g, cur.v[15][1]);
 #pragma unroll
     for (int half = 0; half < 2; ++half) {
       uint32_t cols[4][4];   // [dim j][token t]
@@ -479,6 +565,7 @@ __device__ __forceinline__ void int8_chunk(const DecodeArgs& a, const WorkItem& 
         pv[4 * half + j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(pa, bop, pv[4 * half + j], 0, 0, 0);
       }
     }
+    if (PG_TRACE && g < kTraceSlots) PG_TRACE_MARK(st, kTraceDone + g);
   };
 
   // Software pipeline: the loads of group g+1 are in flight while group g is
@@ -649,6 +736,7 @@ __device__ __forceinline__ void fp16_pages(const DecodeArgs& a, int request, con
     for (int j = 0; j < 4; ++j) consume_point(cur.k[j]);
 #pragma unroll
     for (int k = 0; k < 4; ++k) consume_point(cur.v[k]);
+    if (PG_TRACE && local < kTraceSlots) PG_TRACE_AFTER(st, kTraceK + local, cur.v[3][3]);
     v4f acc = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
     for (int j = 0; j < 4; ++j) acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(qa[j], cur.k[j], acc, 0, 0, 0);
@@ -700,7 +788,10 @@ __device__ __forceinline__ void fp16_pages(const DecodeArgs& a, int request, con
 
   const int local_count = kStrided ? (count - sub + subs - 1) / subs : count;   // this wave's pages
   if (kStrided && local_count <= 0) return;
+  PG_TRACE_AFTER(st, kTraceIds, my_page);
   issue(0, buf[0]);
+  PG_TRACE_MARK(st, kTraceIssued);
+  PG_TRACE_PUT(st, kTracePages, count);
   int slot = 0;
   for (; slot + 2 < local_count; slot += 2) {
     issue(slot + 1, buf[1]);
@@ -1003,12 +1094,18 @@ __device__ __forceinline__ void init_state(HeadState& st) {
   st.l = 0.0f;
 #pragma unroll
   for (int i = 0; i < 8; ++i) st.o[i] = 0.0f;
+#if PG_TRACE
+  st.trace = 0;
+#endif
 }
 
 __global__ __launch_bounds__(kWave * kMaxWavesPerBlock) void decode_partial_kernel(DecodeArgs a) {
   __shared__ __attribute__((aligned(16))) uint8_t lds_all[kMaxWavesPerBlock * kLdsPerWave];
   const int wave = threadIdx.x / kWave;
   const int lane = threadIdx.x % kWave;
+  HeadState st;
+  init_state(st);
+  PG_TRACE_MARK(st, kTraceStart);
   const int kv = blockIdx.y * a.waves_per_block + wave;
   const WorkItem it = a.closed_form
                           ? closed_form_item(blockIdx.x, a.cf_items, a.cf_tail_items, a.cf_tail_begin,
@@ -1016,8 +1113,6 @@ __global__ __launch_bounds__(kWave * kMaxWavesPerBlock) void decode_partial_kern
                                              a.cf_primary_kind)
                           : a.items[blockIdx.x];
   uint8_t* lds = lds_all + wave * kLdsPerWave;
-  HeadState st;
-  init_state(st);
   if (it.kind == PG_KV_INT8) {
     if (a.num_kv_heads == 8)
       int8_chunk<8 * kHeadDim>(a, it, kv, lane, lds, st);
@@ -1048,6 +1143,7 @@ __global__ __launch_bounds__(kWave * kMaxWavesPerBlock) void decode_partial_kern
     fp16_pages(a, it.request, a.tail_k, a.tail_v, a.tail_indices, it.page_begin, it.page_end,
                it.last_page, a.tail_last_len[it.request], kv, lane, lds, st);
   }
+  PG_TRACE_MARK(st, kTraceEnd);
   // partial write: lane (head l/16, n = l%16) owns dims 8n..8n+7.  Layout
   // [request][qo head][item of the request][128] so a combine block reads one
   // (request, head) as a contiguous run.
@@ -1063,6 +1159,16 @@ __global__ __launch_bounds__(kWave * kMaxWavesPerBlock) void decode_partial_kern
     a.partial_m[row] = st.m;
     a.partial_l[row] = l_row;
   }
+#if PG_TRACE
+  if (a.trace != nullptr) {
+    PG_TRACE_PUT(st, kTraceXcc, trace_hwreg_xcc());
+    PG_TRACE_PUT(st, kTraceHwId, trace_hwreg_id());
+    PG_TRACE_PUT(st, kTraceItem, (blockIdx.x << 8) | kv);
+    PG_TRACE_PUT(st, kTraceKind, it.kind);
+    const int64_t w = (static_cast<int64_t>(blockIdx.y) * gridDim.x + blockIdx.x) * a.waves_per_block + wave;
+    a.trace[w * kWave + lane] = st.trace;
+  }
+#endif
 }
 
 // ---------------------------------------------------------------------------
@@ -1221,6 +1327,13 @@ extern "C" int32_t pg_decode_plan(const int32_t* host_indptr, const int32_t* hos
 
 namespace {
 
+#if PG_TRACE
+// Trace buffer of the partial kernel (pg_trace_set_buffer); used by a launch
+// only when it holds a 64-word row for every wave of the grid.
+uint32_t* g_trace = nullptr;
+int64_t g_trace_bytes = 0;
+#endif
+
 struct PartialViews {
   float* o;
   float* m;
@@ -1333,6 +1446,10 @@ int32_t launch_partial(const pg_decode_plan_t* plan, const void* query,
     a.cf_primary_kind = plan->primary_kind;
   }
   const dim3 grid(plan->num_items, plan->num_kv_heads / a.waves_per_block);
+#if PG_TRACE
+  a.trace = static_cast<int64_t>(grid.x) * grid.y * a.waves_per_block * kWave * 4 <= g_trace_bytes
+                ? g_trace : nullptr;
+#endif
   if (start_event || stop_event) {
     // The events take the dispatch's own begin/end timestamps.
     hipExtLaunchKernelGGL(decode_partial_kernel, grid, dim3(kWave * a.waves_per_block), 0,
@@ -1584,3 +1701,17 @@ extern "C" int32_t pg_exact_tail_merge_center(const void* query, const void* exa
                      as_stream(stream), t);
   return check_launch("exact_tail_merge_center");
 }
+
+#if PG_TRACE
+// Trace builds only (bench.py --trace): the device buffer the partial
+// kernel writes its per-wave phase rows into; null or 0 bytes turns the
+// trace off.  A launch whose grid needs more rows than fit writes none.
+extern "C" int32_t pg_trace_set_buffer(void* device_words, int64_t bytes) {
+  clear_error();
+  if (bytes < 0 || (bytes > 0 && device_words == nullptr))
+    return fail(PG_ERROR_INVALID_ARGUMENT, "trace buffer needs a pointer and a nonnegative size");
+  g_trace = static_cast<uint32_t*>(device_words);
+  g_trace_bytes = device_words ? bytes : 0;
+  return PG_OK;
+}
+#endif

@@ -13,10 +13,17 @@
 //    that the decode kernel can be set against the stream of its own
 //    access pattern; ``mode`` varies the lane pattern of the loads.
 // Loaded values are folded into a register and written only under a
-// condition that depends on them, so no load can be removed.
+// condition that depends on them, so no load can be removed; workgroup b
+// writes sink[b] only, and every entry point checks that the sink holds an
+// entry per workgroup of its grid.
+//
+// Built into libpagegauge_bench.so (include/pagegauge_bench.h), bench.py's
+// measurement library, not into the product library.
 #include "pg_common.h"
 
 #include <hip/hip_ext.h>
+
+#include <string>
 
 namespace pg {
 namespace {
@@ -189,14 +196,25 @@ int32_t probe_launch(Kernel kernel, int32_t blocks, void* stream, void* start_ev
   return check_launch(what);
 }
 
+namespace {
+int32_t check_sink(int64_t blocks, int64_t sink_len) {
+  if (blocks > sink_len)
+    return fail(PG_ERROR_INVALID_ARGUMENT,
+                "the sink needs an entry per workgroup (" + std::to_string(blocks) + " > " +
+                    std::to_string(sink_len) + ")");
+  return PG_OK;
+}
+}  // namespace
+
 extern "C" int32_t pg_probe_linear_read(const void* src, int64_t bytes, int32_t* sink,
-                                        int32_t blocks, void* start_event, void* stop_event,
-                                        void* stream) {
+                                        int64_t sink_len, int32_t blocks, void* start_event,
+                                        void* stop_event, void* stream) {
   clear_error();
   if (!src || !sink) return fail(PG_ERROR_INVALID_ARGUMENT, "null tensor pointer");
   if (bytes < 16 || bytes % 16 || reinterpret_cast<uintptr_t>(src) % 16)
     return fail(PG_ERROR_INVALID_ARGUMENT, "the read must be a 16-byte aligned multiple of 16 bytes");
   if (blocks < 1) return fail(PG_ERROR_INVALID_ARGUMENT, "blocks must be positive");
+  if (int32_t rc = check_sink(blocks, sink_len)) return rc;
   return probe_launch(linear_read_kernel, blocks, stream, start_event, stop_event,
                       "probe_linear_read", static_cast<const v4i*>(src), bytes / 16, sink);
 }
@@ -205,7 +223,8 @@ extern "C" int32_t pg_probe_decode_walk(const void* k_pages, const void* v_pages
                                         const int32_t* indices, int32_t pages,
                                         int32_t pages_per_item, int32_t heads_per_block,
                                         int32_t depth, int32_t mode, int32_t* sink,
-                                        void* start_event, void* stop_event, void* stream) {
+                                        int64_t sink_len, void* start_event, void* stop_event,
+                                        void* stream) {
   clear_error();
   if (!k_pages || !v_pages || !indices || !sink)
     return fail(PG_ERROR_INVALID_ARGUMENT, "null tensor pointer");
@@ -219,6 +238,7 @@ extern "C" int32_t pg_probe_decode_walk(const void* k_pages, const void* v_pages
   if (mode < 0 || mode > 2 || (mode == 2 && heads_per_block != 8))
     return fail(PG_ERROR_INVALID_ARGUMENT, "mode must be 0, 1, or 2 with 8 heads per block");
   const dim3 grid(pages / pages_per_item, 8 / heads_per_block);
+  if (int32_t rc = check_sink(grid.x, sink_len)) return rc;   // sink[blockIdx.x]
   const dim3 block(kWave * heads_per_block);
   hipEvent_t start = static_cast<hipEvent_t>(start_event);
   hipEvent_t stop = static_cast<hipEvent_t>(stop_event);
@@ -240,14 +260,15 @@ extern "C" int32_t pg_probe_decode_walk(const void* k_pages, const void* v_pages
 extern "C" int32_t pg_probe_page_walk(const void* k_pages, const void* v_pages,
                                       const int32_t* indices, int32_t pages,
                                       int32_t pages_per_block, int32_t page_bytes,
-                                      int32_t* sink, void* start_event, void* stop_event,
-                                      void* stream) {
+                                      int32_t* sink, int64_t sink_len, void* start_event,
+                                      void* stop_event, void* stream) {
   clear_error();
   if (!k_pages || !v_pages || !indices || !sink)
     return fail(PG_ERROR_INVALID_ARGUMENT, "null tensor pointer");
   if (pages < 1 || pages_per_block < 1 || page_bytes < 16 || page_bytes % 16)
     return fail(PG_ERROR_INVALID_ARGUMENT, "pages, pages per block and page bytes must be positive");
   const int32_t blocks = (pages + pages_per_block - 1) / pages_per_block;
+  if (int32_t rc = check_sink(blocks, sink_len)) return rc;
   return probe_launch(page_walk_kernel, blocks, stream, start_event, stop_event, "probe_page_walk",
                       static_cast<const int8_t*>(k_pages), static_cast<const int8_t*>(v_pages),
                       indices, pages, pages_per_block, page_bytes, sink);

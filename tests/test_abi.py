@@ -1,7 +1,8 @@
 """The C-ABI boundary on the CPU: the library loads, exports every symbol
-``include/pagegauge_hip.h`` declares, the ctypes prototypes agree with the
-header, and the host-only entry points validate as documented.  No GPU
-compute is called here."""
+``include/pagegauge_hip.h`` declares (and nothing else), the ctypes
+prototypes agree with the header, and the host-only entry points validate as
+documented; likewise bench.py's probe library against
+``include/pagegauge_bench.h``.  No GPU compute is called here."""
 
 from __future__ import annotations
 
@@ -17,11 +18,12 @@ from pagegauge_amd import _capi
 
 ROOT = Path(__file__).resolve().parents[1]
 HEADER = ROOT / "include" / "pagegauge_hip.h"
+BENCH_HEADER = ROOT / "include" / "pagegauge_bench.h"
 
 
-def _declarations() -> dict[str, int]:
+def _declarations(header=HEADER) -> dict[str, int]:
     """name -> parameter count of every function declared in the header."""
-    text = re.sub(r"/\*.*?\*/", "", HEADER.read_text(), flags=re.S)
+    text = re.sub(r"/\*.*?\*/", "", header.read_text(), flags=re.S)
     out = {}
     for match in re.finditer(r"^(?:const\s+)?[a-z_0-9]+\s*\*?\s*(pg_[a-z_0-9]+)\s*\(([^;]*?)\)\s*;",
                              text, flags=re.M | re.S):
@@ -51,6 +53,22 @@ def test_ctypes_prototypes_match_header_arity():
     assert set(_capi.PROTOTYPES) == set(declared)
     for name, (_, argtypes) in _capi.PROTOTYPES.items():
         assert len(argtypes) == declared[name], name
+
+
+def test_bench_library_exports_its_header_and_nothing_of_the_product():
+    """The probes live in libpagegauge_bench.so; the product exports none of
+    them.  pg_trace_set_buffer is declared there too but exported only by the
+    trace build of the product library."""
+    declared = _declarations(BENCH_HEADER)
+    assert {"pg_probe_linear_read", "pg_probe_page_walk", "pg_probe_decode_walk"} <= set(declared)
+    exported = subprocess.run(["nm", "-D", "--defined-only", str(_capi.BENCH_LIBRARY_PATH)],
+                              capture_output=True, text=True, check=True).stdout
+    public = set(re.findall(r" T (pg_[a-z_0-9]+)$", exported, flags=re.M))
+    assert public == set(declared) - {"pg_trace_set_buffer"}
+    for name, (_, argtypes) in {**_capi.BENCH_PROTOTYPES, **_capi.TRACE_PROTOTYPES}.items():
+        assert len(argtypes) == declared[name], name
+    assert not any(name.startswith("pg_probe") for name in _declarations())
+    assert _capi.bench_library().pg_abi_version() == _capi.ABI_VERSION
 
 
 def test_library_loads_and_reports_abi_version():

@@ -237,13 +237,23 @@ def test_page_id_check_is_opt_in(monkeypatch):
     ((16, 16, 16, 2, 2, 1, 0), "heads_per_block"),
     ((16, 16, 16, 8, 3, 1, 0), "depth"),
     ((16, 16, 16, 4, 2, 2, 0), "mode"),                # whole pages need 8 heads per block
+    ((16, 64, 4, 4, 2, 0, 0), "an entry per workgroup"),  # 16 workgroups, a 15-entry sink
 ])
 def test_decode_walk_probe_rejects(args, message):
     """Argument checks of pg_probe_decode_walk run before any launch (no GPU
     needed); fake non-null pointers never reach a kernel."""
-    lib = _capi.library()
+    lib = _capi.bench_library()
     ptr, pages, per_item, heads, depth, mode, _ = args
     fake = ptr or None
     rc = lib.pg_probe_decode_walk(fake, fake, fake, pages, per_item, heads, depth, mode, fake,
-                                  None, None, None)
-    assert rc == 1 and message in _capi.last_error()
+                                  15, None, None, None)
+    assert rc == 1 and message in lib.pg_last_error().decode()
+
+
+def test_read_probes_reject_a_short_sink():
+    lib = _capi.bench_library()
+    fake = 16
+    assert lib.pg_probe_linear_read(fake, 1 << 20, fake, 511, 512, None, None, None) == 1
+    assert "an entry per workgroup (512 > 511)" in lib.pg_last_error().decode()
+    assert lib.pg_probe_page_walk(fake, fake, fake, 40, 4, 16384, fake, 9, None, None, None) == 1
+    assert "(10 > 9)" in lib.pg_last_error().decode()

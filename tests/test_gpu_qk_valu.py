@@ -2,7 +2,7 @@
 pagegauge_amd.build --variant qk_valu``) computes the same integer digit dot
 products as the product's i8 MFMA, so its decode outputs must be bit-identical
 to the product's on the same plan and inputs.  Skipped when the alternative
-build is absent."""
+build is absent or older than the sources (it is built on request only)."""
 
 from __future__ import annotations
 
@@ -18,10 +18,10 @@ pytestmark = pytest.mark.gpu
 
 @pytest.fixture(scope="module")
 def valu_library():
-    path = build.variant_library("qk_valu")
-    if not path.exists():
-        pytest.skip("qk_valu alternative build not present")
-    return _capi.load_library(path)
+    if not build.variant_is_current("qk_valu"):
+        pytest.skip("qk_valu alternative build absent or stale "
+                    "(python -m pagegauge_amd.build --variant qk_valu)")
+    return _capi.load_library(build.variant_library("qk_valu"))
 
 
 def _run(lib, dec, w, out, lse):
