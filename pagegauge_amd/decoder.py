@@ -335,12 +335,17 @@ class Fp16Cache:
 class GaugeCache:
     """PageGauge storage (scripts/benchmark_page_gauge_transformer.py:321-380):
     INT8 codes [L, B*P, 16, Hkv, 128], scales [L, B*P, Hkv], per-request
-    centers [L, B, Hkv, 128] and the exact FP16 ring [L, B*E, 16, Hkv, 128]
-    (E = prefix pages + tail ring pages)."""
+    centers [L, B, Hkv, 128] and the exact FP16 pages [L, B*E, 16, Hkv, 128],
+    E = S prefix (sink) pages + A static-suffix pages (the A pages before
+    ``initial_context_pages``, kept exact for the whole decode) + the tail
+    ring, in that order per request."""
 
     def __init__(self, config: DecoderConfig, batch_size: int, pages: int,
-                 exact_tail_pages: int, exact_sink_pages: int = 0, device="cuda") -> None:
-        pt.validate_exact_prefix_pages(exact_sink_pages)
+                 exact_tail_pages: int, exact_sink_pages: int = 0, device="cuda",
+                 exact_static_suffix_pages: int = 0,
+                 initial_context_pages: Optional[int] = None) -> None:
+        layout = pt.ExactPageLayout.checked(exact_sink_pages, exact_static_suffix_pages,
+                                            initial_context_pages, exact_tail_pages)
         if exact_tail_pages <= 0:
             raise ValueError("at least one tail-ring page is required")
         L, hkv = config.layers, config.kv_heads
@@ -353,7 +358,10 @@ class GaugeCache:
         self.value_center = torch.zeros_like(self.key_center)
         self.exact_tail_pages = exact_tail_pages
         self.exact_sink_pages = exact_sink_pages
-        self.exact_storage_pages_per_request = exact_tail_pages + exact_sink_pages
+        self.exact_static_suffix_pages = layout.suffix
+        self.initial_context_pages = layout.initial
+        self.exact_fixed_pages = layout.fixed
+        self.exact_storage_pages_per_request = layout.storage
         ring = batch_size * self.exact_storage_pages_per_request
         self.exact_key = torch.zeros(L, ring, PAGE, hkv, DIM, device=device, dtype=torch.float16)
         self.exact_value = torch.zeros_like(self.exact_key)
@@ -371,7 +379,8 @@ class GaugeCache:
     def populate(self, layer: int, request: int, key: torch.Tensor, value: torch.Tensor) -> None:
         """Cache a token-major prefix [T, Hkv, 128] of whole pages: exact
         centers, INT8 codes and scales of every page, and the centered FP16
-        copies of its exact pages (the sink prefix and the last tail pages)
+        copies of its exact pages (the sink prefix, the static suffix and the
+        last tail pages) in their slots
         (diagnostics/benchmark_backend_exclusive.py:427-506)."""
         tokens = key.shape[0]
         pages = tokens // PAGE
@@ -379,6 +388,8 @@ class GaugeCache:
             raise ValueError("prefix must be whole pages within the cache capacity")
         if pages <= self.exact_tail_pages + self.exact_sink_pages:
             raise ValueError("fixture must contain at least one quantized old page")
+        if self.exact_static_suffix_pages and pages < self.initial_context_pages:
+            raise ValueError("the static suffix lies beyond the cached prefix")
         from . import _capi
         need = int(_capi.library().pg_token_major_centers_workspace_bytes(tokens, key.shape[1]))
         if self._center_workspace is None or self._center_workspace.numel() < need:
@@ -386,11 +397,13 @@ class GaugeCache:
         kc, vc = self.key_center[layer, request], self.value_center[layer, request]
         token_major_centers(key, value, kc, vc, self._center_workspace)
         exact_map = torch.full((pages,), -1, dtype=torch.int32)
-        exact_logical = list(range(self.exact_sink_pages)) + list(
-            range(pages - self.exact_tail_pages, pages))
-        for logical in exact_logical:
+        partition = pt.page_gauge_logical_partition(
+            pages, self.exact_tail_pages, self.exact_sink_pages, PAGE,
+            self.exact_static_suffix_pages, self.initial_context_pages)
+        for logical in partition["exact_logical_pages"]:
             exact_map[logical] = pt.exact_physical_page_index(
-                request, logical, self.exact_tail_pages, self.exact_sink_pages)
+                request, logical, self.exact_tail_pages, self.exact_sink_pages,
+                self.exact_static_suffix_pages, self.initial_context_pages)
         base = request * self.pages_per_request
         prefill_page_gauge(key, value, kc, vc,
                            self.key_codes[layer, base:base + pages],
@@ -488,13 +501,19 @@ class PageGaugeDecoder:
                  rope_cos: torch.Tensor, rope_sin: torch.Tensor, exact_tail: int = 256,
                  split_pages: int = 0, batch_size: int = 1, exact_sink_pages: int = 0,
                  workspace_bytes: int = 128 * 1024 * 1024, fused: Optional[bool] = None,
-                 tail_attention: str = "segmented", fused_append: Optional[bool] = None) -> None:
+                 tail_attention: str = "segmented", fused_append: Optional[bool] = None,
+                 exact_static_suffix_pages: int = 0,
+                 initial_context_pages: Optional[int] = None) -> None:
         if backend not in ("page_gauge", "fp16"):
             raise ValueError(f"unknown backend {backend}")
         if tail_attention not in ("segmented", "heterogeneous"):
             raise ValueError(f"unknown exact-tail attention path {tail_attention}")
         if tail_attention == "heterogeneous" and exact_sink_pages:
             raise ValueError("exact prefix pages require the segmented flashinfer_merge path")
+        layout = pt.ExactPageLayout.checked(exact_sink_pages, exact_static_suffix_pages,
+                                            initial_context_pages, exact_tail // PAGE)
+        if layout.suffix and tail_attention != "segmented":
+            raise ValueError("an exact static suffix requires the segmented flashinfer_merge path")
         self.tail_attention = tail_attention
         if batch_size <= 0:
             raise ValueError("batch size must be positive")
@@ -513,7 +532,11 @@ class PageGaugeDecoder:
         self.batch_size = batch_size
         self.max_pages = math.ceil(max_context / PAGE)
         self.exact_tail_pages = exact_tail // PAGE
-        self.exact_sink_pages = pt.validate_exact_prefix_pages(exact_sink_pages)
+        self.exact_sink_pages = layout.prefix
+        self.exact_static_suffix_pages = layout.suffix
+        self.initial_context_pages = layout.initial
+        self.exact_fixed_pages = layout.fixed           # slots that never move: S + A
+        exact_slots = layout.fixed + self.exact_tail_pages
         self.split_pages = split_pages
         self.rope_cos, self.rope_sin = rope_cos, rope_sin
         device = rope_cos.device
@@ -525,15 +548,22 @@ class PageGaugeDecoder:
                 raise ValueError("PageGauge cache must use request-major pages and per-request "
                                  "[L,B,Hkv,D] centers")
             if (cache.exact_tail_pages != self.exact_tail_pages
-                    or cache.exact_sink_pages != self.exact_sink_pages):
-                raise ValueError("exact cache must contain the configured fixed prefix "
+                    or cache.exact_sink_pages != self.exact_sink_pages
+                    or cache.exact_static_suffix_pages != self.exact_static_suffix_pages
+                    or cache.initial_context_pages != self.initial_context_pages):
+                raise ValueError("exact cache must contain the configured fixed prefix/suffix "
                                  "pages followed by tail-ring pages")
             self.exact_ring_pages = pt.request_major_exact_page_table(
                 batch_size, self.max_pages, self.exact_tail_pages, self.exact_sink_pages,
-                device=device)
-            self.exact_plan_pages = torch.empty(
-                batch_size, self.exact_tail_pages + self.exact_sink_pages, device=device,
-                dtype=torch.int32)
+                self.exact_static_suffix_pages, self.initial_context_pages, device=device)
+            self.exact_plan_pages = torch.empty(batch_size, exact_slots, device=device,
+                                                dtype=torch.int32)
+            # with a static suffix the INT8 pages are no longer one run of the
+            # logical table: they are gathered into a table of their own
+            self.old_plan_pages = (torch.empty_like(self.all_pages)
+                                   if self.exact_static_suffix_pages else None)
+            self.old_layout_signature: Optional[tuple] = None
+            self.old_page_table_updates = 0
             if tail_attention == "heterogeneous":
                 # one unified table: INT8 code pages, then the exact ring
                 # (scripts/benchmark_page_gauge_transformer.py:1817-1830, :2085-2110)
@@ -545,8 +575,7 @@ class PageGaugeDecoder:
                 self.decode = HeterogeneousDecodeWrapper(self.workspace)
             else:
                 self.old_table = SegmentTable(batch_size, self.max_pages, device)
-                self.exact_table = SegmentTable(batch_size,
-                                                self.exact_tail_pages + self.exact_sink_pages, device)
+                self.exact_table = SegmentTable(batch_size, exact_slots, device)
                 self.decode = PageGaugeSegmentedDecode(self.workspace)
         else:
             if not isinstance(cache, Fp16Cache) or cache.pages_per_request != self.max_pages:
@@ -618,7 +647,9 @@ class PageGaugeDecoder:
             self.plan_signature_value = ("fp16", self.table.signature)
             return
         partition = pt.page_gauge_logical_partition(pages, self.exact_tail_pages,
-                                                    self.exact_sink_pages, last_len)
+                                                    self.exact_sink_pages, last_len,
+                                                    self.exact_static_suffix_pages,
+                                                    self.initial_context_pages)
         self.tail_logical_begin = int(partition["tail_logical_begin"])
         self.old_pages = int(partition["old_page_count"])
         self.exact_pages = int(partition["exact_page_count"])
@@ -641,16 +672,32 @@ class PageGaugeDecoder:
                 self.kernel_replans += 1
             self.plan_signature_value = ("heterogeneous", self.table.signature)
             return
-        old_begin = partition["old_logical_pages"][0]
-        old_indices = self.all_pages[:, old_begin:old_begin + self.old_pages]
-        changed = self.old_table.plan(old_indices, old_tokens, PAGE, self.split_pages)
+        old_epoch = None
+        if self.old_plan_pages is not None:
+            # for a fixed prefix, suffix and ring the INT8 set grows one page
+            # at a time, so its size names it
+            layout = (self.old_pages,)
+            if layout != self.old_layout_signature:
+                old_indices = pt.write_page_gauge_old_page_table(
+                    self.old_plan_pages, self.all_pages, partition["old_logical_pages"])
+                self.old_layout_signature = layout
+                self.old_page_table_updates += 1
+            else:
+                old_indices = self.old_plan_pages[:, :self.old_pages]
+            old_epoch = self.old_page_table_updates
+        else:
+            old_begin = partition["old_logical_pages"][0]
+            old_indices = self.all_pages[:, old_begin:old_begin + self.old_pages]
+        changed = self.old_table.plan(old_indices, old_tokens, PAGE, self.split_pages,
+                                      page_table_epoch=old_epoch)
         epoch = None
-        if self.exact_sink_pages:
+        if self.exact_fixed_pages:
             layout = (self.tail_logical_begin, pages, self.exact_pages)
             if layout != self.exact_layout_signature:
                 exact_indices = pt.write_exact_prefix_tail_page_table(
                     self.exact_plan_pages, self.exact_ring_pages, self.tail_logical_begin, pages,
-                    self.exact_sink_pages)
+                    self.exact_sink_pages, self.exact_static_suffix_pages,
+                    self.initial_context_pages)
                 self.exact_layout_signature = layout
                 self.exact_page_table_updates += 1
             else:
@@ -685,7 +732,7 @@ class PageGaugeDecoder:
             query, key, value, self.rope_cos, self.rope_sin, self.device_position,
             c.key_center[layer], c.value_center[layer], self.rotated_query, c.exact_key[layer],
             c.exact_value[layer], c.key_codes[layer], c.value_codes[layer], c.key_scales[layer],
-            c.value_scales[layer], self.exact_sink_pages)
+            c.value_scales[layer], self.exact_fixed_pages)
 
     def _qkv_append(self, layer: int) -> None:
         """QKV projection + RoPE + cache append in one launch."""
@@ -705,7 +752,7 @@ class PageGaugeDecoder:
                         value_pages=c.exact_value[layer], key_center=c.key_center[layer],
                         value_center=c.value_center[layer],
                         pages_per_request=c.exact_storage_pages_per_request,
-                        sink_pages=self.exact_sink_pages,
+                        sink_pages=self.exact_fixed_pages,
                         capacity_tokens=c.pages_per_request * PAGE, **common)
 
     def attention(self, layer: int) -> torch.Tensor:
@@ -878,11 +925,13 @@ class PageGaugeDecoder:
 
 def build_decoders(weights: DecoderWeights, prompt: torch.Tensor, decode_steps: int,
                    exact_tail: int = 256, backends=("page_gauge", "fp16"), split_pages: int = 0,
-                   exact_sink_pages: int = 0):
+                   exact_sink_pages: int = 0, exact_static_suffix_pages: int = 0):
     """Prefill ``prompt`` [T] or [B, T] (T a multiple of 16; every request the
     same length, as the decoder steps requests in lockstep) once per request,
     populate one cache per backend from the same rotated K/V, and return
-    ``(first_tokens [B], prefill_logits [B,V], {backend: decoder})``."""
+    ``(first_tokens [B], prefill_logits [B,V], {backend: decoder})``.  A
+    static suffix keeps the last ``exact_static_suffix_pages`` pages of the
+    prompt exact (the initial context is the prompt)."""
     cfg = weights.config
     prompts = prompt.reshape(1, -1) if prompt.dim() == 1 else prompt
     batch, count = int(prompts.shape[0]), int(prompts.shape[1])
@@ -894,9 +943,10 @@ def build_decoders(weights: DecoderWeights, prompt: torch.Tensor, decode_steps: 
     cos, sin = rope_tables(max_context, cfg.rope_theta)
     cos, sin = cos.to(device), sin.to(device)
     caches = {}
+    initial = count // PAGE if exact_static_suffix_pages else None
     if "page_gauge" in backends:
         caches["page_gauge"] = GaugeCache(cfg, batch, pages, exact_tail // PAGE, exact_sink_pages,
-                                          device)
+                                          device, exact_static_suffix_pages, initial)
     if "fp16" in backends:
         caches["fp16"] = Fp16Cache(cfg, batch, pages, device)
 
@@ -909,8 +959,10 @@ def build_decoders(weights: DecoderWeights, prompt: torch.Tensor, decode_steps: 
         logits.append(prefill(weights, prompts[request].to(device), cos, sin, on_layer))
     logits = torch.cat(logits)
     first = logits.argmax(dim=-1)
-    decoders = {name: PageGaugeDecoder(weights, cache, name, max_context, cos, sin, exact_tail,
-                                       split_pages, batch,
-                                       exact_sink_pages if name == "page_gauge" else 0)
+    decoders = {name: PageGaugeDecoder(
+                    weights, cache, name, max_context, cos, sin, exact_tail, split_pages, batch,
+                    exact_sink_pages if name == "page_gauge" else 0,
+                    exact_static_suffix_pages=exact_static_suffix_pages if name == "page_gauge" else 0,
+                    initial_context_pages=initial if name == "page_gauge" else None)
                 for name, cache in caches.items()}
     return first, logits, decoders

@@ -71,7 +71,7 @@ def max_abs(a, b) -> float:
     return float(np.abs(a.astype(np.float64) - b.astype(np.float64)).max())
 
 
-def dense_reference_class(dec, dtype=None, attention_output="kernel"):
+def dense_reference_class(dec, dtype=None, attention_output="kernel", tables="decoder"):
     """A ``dec.PageGaugeDecoder`` whose attention is the dense softmax, in
     ``dtype`` (float32 by default), over the reconstructed cache: K = c_K +
     s*Z for old pages and c_K + ring for tail pages, V likewise, from the same
@@ -87,7 +87,13 @@ def dense_reference_class(dec, dtype=None, attention_output="kernel"):
     projection as one float32 torch product of the FP16-rounded, or unrounded,
     dense attention (same epilogue: the projection rounded to FP16, then the
     FP16 residual add).  The two differ only by the FP16 rounding of the
-    attention output, which measures the decoder's rounding floor."""
+    attention output, which measures the decoder's rounding floor.
+
+    ``tables``: "decoder" reads the context through the decoder's own segment
+    tables; "logical" rebuilds it from the page classes instead (the pinned
+    ``page_table`` partition and exact-slot functions: every logical page of
+    the context once, from the INT8 pool or from its exact slot), so that a
+    wrong table cannot agree with itself."""
     import math
 
     import torch
@@ -125,12 +131,33 @@ def dense_reference_class(dec, dtype=None, attention_output="kernel"):
                            norm_weight=w["post_norm"], eps=cfg.rms_eps, swiglu=True)
             dec.projection(w["down"], self._activation, self._hidden, residual=self._hidden)
 
+        def _logical_tables(self, b):
+            from pagegauge_amd import page_table as pt
+
+            last = int(self.exact_table.host_last_len[b])
+            pages = self.current_pages
+            part = pt.page_gauge_logical_partition(
+                pages, self.exact_tail_pages, self.exact_sink_pages, last,
+                self.exact_static_suffix_pages, self.initial_context_pages)
+            old = [b * self.max_pages + p for p in part["old_logical_pages"]]
+            exact = [pt.exact_physical_page_index(b, p, self.exact_tail_pages,
+                                                  self.exact_sink_pages,
+                                                  self.exact_static_suffix_pages,
+                                                  self.initial_context_pages)
+                     for p in part["exact_logical_pages"]]
+            assert part["exact_logical_pages"][-1] == pages - 1   # the newest page is exact
+            device = self.cache.key_codes.device
+            return (torch.tensor(old, device=device), torch.tensor(exact, device=device), last)
+
         def _dense(self, layer):
             c = self.cache
             b = 0
-            old = self.old_table.active_indices().long()
-            tail = self.exact_table.active_indices().long()
-            last = int(self.exact_table.host_last_len[b])
+            if tables == "logical":
+                old, tail, last = self._logical_tables(b)
+            else:
+                old = self.old_table.active_indices().long()
+                tail = self.exact_table.active_indices().long()
+                last = int(self.exact_table.host_last_len[b])
             kc = c.key_center[layer, b].to(dtype)
             vc = c.value_center[layer, b].to(dtype)
             k_old = c.key_codes[layer][old].to(dtype) * c.key_scales[layer][old].to(dtype)[:, None, :, None]

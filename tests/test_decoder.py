@@ -68,7 +68,7 @@ class _FakeSegmented:
                            tail_indptr.tolist(), tail_indices.tolist(), tail_last.tolist()))
 
 
-def _plan_only_decoder(batch, max_pages, tail_pages, sink_pages):
+def _plan_only_decoder(batch, max_pages, tail_pages, sink_pages, suffix_pages=0, initial=None):
     d = dec.PageGaugeDecoder.__new__(dec.PageGaugeDecoder)
     d.backend = "page_gauge"
     d.tail_attention = "segmented"
@@ -76,13 +76,20 @@ def _plan_only_decoder(batch, max_pages, tail_pages, sink_pages):
     d.decoder_plan_calls = d.kernel_replans = d.exact_page_table_updates = 0
     d.max_pages, d.batch_size = max_pages, batch
     d.exact_tail_pages, d.exact_sink_pages, d.split_pages = tail_pages, sink_pages, 0
+    d.exact_static_suffix_pages, d.initial_context_pages = suffix_pages, initial
+    d.exact_fixed_pages = sink_pages + suffix_pages
+    slots = tail_pages + sink_pages + suffix_pages
     d.all_pages = pt.request_major_page_table(batch, max_pages, device="cpu")
     d.exact_ring_pages = pt.request_major_exact_page_table(batch, max_pages, tail_pages,
-                                                           sink_pages, device="cpu")
-    d.exact_plan_pages = torch.empty(batch, tail_pages + sink_pages, dtype=torch.int32)
+                                                           sink_pages, suffix_pages, initial,
+                                                           device="cpu")
+    d.exact_plan_pages = torch.empty(batch, slots, dtype=torch.int32)
+    d.old_plan_pages = torch.empty_like(d.all_pages) if suffix_pages else None
+    d.old_layout_signature = None
+    d.old_page_table_updates = 0
     d.exact_layout_signature = None
     d.old_table = dec.SegmentTable(batch, max_pages, "cpu")
-    d.exact_table = dec.SegmentTable(batch, tail_pages + sink_pages, "cpu")
+    d.exact_table = dec.SegmentTable(batch, slots, "cpu")
     d.decode = _FakeSegmented()
     return d
 
@@ -106,6 +113,38 @@ def test_decoder_plan_excludes_sink_from_old_and_prepends_it_to_exact():
     assert d.exact_table.last_len.tolist() == [15, 15]
     assert d.kernel_replans == 1                     # same structure: no re-plan
     assert len(d.decode.calls) == 1
+
+
+def test_decoder_plan_fixed_suffix_uses_exact_once_tables():
+    """reference tests/test_page_gauge_transformer.py:377-427 (tail 2, prefix
+    1, static suffix 2, initial context 8 pages; capacity 12 here so that the
+    tail can move past the suffix)."""
+    d = _plan_only_decoder(batch=1, max_pages=12, tail_pages=2, sink_pages=1, suffix_pages=2,
+                           initial=8)
+    d.plan(8 * PAGE)
+    old_indptr, old_indices, old_last, exact_indptr, exact_indices, exact_last = d.decode.calls[-1]
+    assert old_indices == [1, 2, 3, 4, 5]
+    assert exact_indices == [0, 1, 2]
+    assert d.old_pages * PAGE == 5 * PAGE and d.exact_pages == 3
+    d.plan(8 * PAGE + 1)
+    old_indptr, old_indices, old_last, exact_indptr, exact_indices, exact_last = d.decode.calls[-1]
+    assert old_indices == [1, 2, 3, 4, 5]
+    assert exact_indices == [0, 1, 2, 3]
+    assert len(set(exact_indices)) == 4
+    assert d.old_pages + d.exact_pages == 9
+    assert exact_last == [1]
+    # the tail moves past the suffix; the suffix (pages 6, 7: slots 1, 2) stays
+    d.plan(10 * PAGE)
+    old_indices, exact_indices = d.decode.calls[-1][1], d.decode.calls[-1][4]
+    assert old_indices == [1, 2, 3, 4, 5]
+    assert exact_indices == [0, 1, 2, 3 + 8 % 2, 3 + 9 % 2]
+    # one page later page 8 leaves the ring for the INT8 table
+    d.plan(10 * PAGE + 1)
+    old_indices, exact_indices = d.decode.calls[-1][1], d.decode.calls[-1][4]
+    assert old_indices == [1, 2, 3, 4, 5, 8]
+    assert exact_indices == [0, 1, 2, 3 + 9 % 2, 3 + 10 % 2]
+    assert d.old_pages + d.exact_pages == 11
+    assert d.old_page_table_updates == 2
 
 
 def test_decoder_plan_replans_once_per_page_window():
