@@ -90,7 +90,8 @@ def parse_args() -> argparse.Namespace:
                         "trace_conditional_scales): the variant name; B1/49K, 16K and 4K, "
                         "cold calls; prints one JSON line")
     p.add_argument("--trace-calls", type=int, default=20)
-    p.add_argument("--workload", choices=("b1_49k", "config1", "serving_b256"), default="b1_49k",
+    p.add_argument("--workload", choices=("b1_49k", "b1_16k", "config1", "serving_b256"),
+                   default="b1_49k",
                    help="workload of the --pmc-calls driver (config1: B=1, 4096 tokens; "
                         "serving_b256: 256 ragged requests)")
     p.add_argument("--pmc-calls", type=int, default=0,
@@ -1352,6 +1353,9 @@ def main() -> int:
     t_setup = time.perf_counter()
     if args.pmc_calls and args.workload == "config1":
         w = workloads.single_4k(args.seed, device=device, with_fp16_copy=not args.no_fp16)
+    elif args.pmc_calls and args.workload == "b1_16k":
+        w = workloads.build_decode_workload([16384 + 16], args.seed, device=device,
+                                            with_fp16_copy=not args.no_fp16)
     elif args.pmc_calls and args.workload == "serving_b256":
         w = workloads.serving_b256(device=device, with_fp16_copy=not args.no_fp16)
     else:
