@@ -882,19 +882,20 @@ __device__ __forceinline__ void combine_unit(const CombineArgs& a, int row_head,
   const float* pl = a.partial_l + base;
   const float* po = a.partial_o + base * kHeadDim + dim;
 
-  float center4[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-  if (active && tid < kCombineCols && a.value_center != nullptr) {
-    const uint16_t* cv = a.value_center + request * a.center_batch_stride + (qh / kGqa) * kHeadDim +
-                         32 * quarter + 4 * tid;
-    const uint2 bits = *reinterpret_cast<const uint2*>(cv);
-    center4[0] = half_bits_to_float(static_cast<uint16_t>(bits.x));
-    center4[1] = half_bits_to_float(static_cast<uint16_t>(bits.x >> 16));
-    center4[2] = half_bits_to_float(static_cast<uint16_t>(bits.y));
-    center4[3] = half_bits_to_float(static_cast<uint16_t>(bits.y >> 16));
-  }
-  int count = 0;
-  if (active)
-    count = a.uniform_items > 0 ? a.uniform_items : a.item_ptr[request + 1] - a.item_ptr[request];
+  // The value center: every thread loads the 8-byte slice of column tid % 8
+  // unconditionally (with no center, the first 8 bytes of this row's
+  // partials, whose bits are dropped) and converts it only after the partial
+  // rows are requested.  A conditional load compiles to a branch that waits
+  // for it, which put a whole round trip in front of the partial loads.
+  const bool has_center = a.value_center != nullptr;
+  const uint16_t* cv = has_center
+                           ? a.value_center + request * a.center_batch_stride +
+                                 (qh / kGqa) * kHeadDim + 32 * quarter + 4 * (tid % kCombineCols)
+                           : reinterpret_cast<const uint16_t*>(a.partial_o + base * kHeadDim);
+  uint2 center_bits = *reinterpret_cast<const uint2*>(cv);
+  // the request's item count, used only after the rows are requested
+  int item_begin = a.item_ptr[request];
+  int item_end = a.item_ptr[request + 1];
   float4 ov[kCombineInRegs];
   float mv[kCombineInRegs], lv[kCombineInRegs];
 #pragma unroll
@@ -905,6 +906,18 @@ __device__ __forceinline__ void combine_unit(const CombineArgs& a, int row_head,
                     : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
     mv[k] = planned ? pm[j] : kNegInf;
     lv[k] = planned ? pl[j] : 0.0f;
+  }
+  consume_point(center_bits.x);   // waits for the center and the count here, the rows in flight
+  consume_point(center_bits.y);
+  consume_point(item_begin);
+  consume_point(item_end);
+  const int count = !active ? 0 : a.uniform_items > 0 ? a.uniform_items : item_end - item_begin;
+  float center4[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+  if (has_center) {
+    center4[0] = half_bits_to_float(static_cast<uint16_t>(center_bits.x));
+    center4[1] = half_bits_to_float(static_cast<uint16_t>(center_bits.x >> 16));
+    center4[2] = half_bits_to_float(static_cast<uint16_t>(center_bits.y));
+    center4[3] = half_bits_to_float(static_cast<uint16_t>(center_bits.y >> 16));
   }
   float local_max = kNegInf;
 #pragma unroll
@@ -1026,15 +1039,16 @@ __global__ __launch_bounds__(kCombineThreads) void combine_rows_kernel(CombineAr
   const float* pl = a.partial_l + base;
   const float* po = a.partial_o + base * kHeadDim + 2 * lane;
 
-  float center2[2] = {0.0f, 0.0f};
-  if (a.value_center != nullptr) {
-    const uint32_t bits = *reinterpret_cast<const uint32_t*>(
-        a.value_center + request * a.center_batch_stride + (qh / kGqa) * kHeadDim + 2 * lane);
-    center2[0] = half_bits_to_float(static_cast<uint16_t>(bits));
-    center2[1] = half_bits_to_float(static_cast<uint16_t>(bits >> 16));
-  }
-  const int count =
-      a.uniform_items > 0 ? a.uniform_items : a.item_ptr[request + 1] - a.item_ptr[request];
+  // the value center, loaded unconditionally and converted after the
+  // partial rows are requested (as in combine_unit)
+  const bool has_center = a.value_center != nullptr;
+  uint32_t center_bits = *(has_center
+                               ? reinterpret_cast<const uint32_t*>(
+                                     a.value_center + request * a.center_batch_stride +
+                                     (qh / kGqa) * kHeadDim + 2 * lane)
+                               : reinterpret_cast<const uint32_t*>(po));
+  int item_begin = a.item_ptr[request];
+  int item_end = a.item_ptr[request + 1];
   float2 ov[kSlots];
   float mv[kSlots], lv[kSlots];
 #pragma unroll
@@ -1044,6 +1058,15 @@ __global__ __launch_bounds__(kCombineThreads) void combine_rows_kernel(CombineAr
                     : make_float2(0.0f, 0.0f);
     mv[j] = planned ? pm[j] : kNegInf;
     lv[j] = planned ? pl[j] : 0.0f;
+  }
+  consume_point(center_bits);
+  consume_point(item_begin);
+  consume_point(item_end);
+  const int count = a.uniform_items > 0 ? a.uniform_items : item_end - item_begin;
+  float center2[2] = {0.0f, 0.0f};
+  if (has_center) {
+    center2[0] = half_bits_to_float(static_cast<uint16_t>(center_bits));
+    center2[1] = half_bits_to_float(static_cast<uint16_t>(center_bits >> 16));
   }
   float m = kNegInf;
 #pragma unroll
