@@ -211,7 +211,10 @@ int32_t pg_token_major_centers(const void* key, int64_t key_token_stride, const 
  * belong to the current device.  Every call on a GPU shares that GPU's
  * array: calls that overlap on one GPU (other streams, other threads) race
  * and must be serialised by the caller.  Results are bit-identical to
- * pg_token_major_centers. */
+ * pg_token_major_centers.  The first call on a device resolves that
+ * device's scratch address (hipGetSymbolAddress) and caches it: make it
+ * once before capturing the call in a graph, and do not reset the device
+ * (hipDeviceReset) while the library is loaded. */
 int64_t pg_token_major_centers_noalloc_max_bytes(void);
 int32_t pg_token_major_centers_noalloc(const void* key, int64_t key_token_stride,
                                        const void* value, int64_t value_token_stride,
@@ -312,8 +315,10 @@ int32_t pg_decode_plan(const int32_t* host_indptr, const int32_t* host_last_page
  * 12 * items_capacity int32) {request, kind (PG_KV_*), segment (0 primary,
  * 1 tail), page_begin, page_end (positions in indices/tail_indices), last
  * position of the segment, item index inside its request, items of the
- * request, position of the request's first page in the segment, 3
- * reserved}; item_ptr_out (if != NULL) receives [B+1] offsets of each
+ * request, position of the request's first page in the segment, the
+ * planner's weight per page of the item (2 for FP16 pages planned beside
+ * INT8 pages: a tail, or a heterogeneous table's hinted exact pages; else
+ * 1), 2 reserved}; item_ptr_out (if != NULL) receives [B+1] offsets of each
  * request's items.  Call once with items_out NULL to learn plan->num_items.  For inspection and tests of
  * the scheduler; no reference counterpart (FlashInfer's plan info is opaque). */
 int32_t pg_decode_plan_host(const int32_t* host_indptr, const int32_t* host_last_page_len,

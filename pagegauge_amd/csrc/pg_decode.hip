@@ -1332,7 +1332,7 @@ extern "C" int32_t pg_decode_plan(const int32_t* host_indptr, const int32_t* hos
                                         std::to_string(p.workspace_bytes) + " bytes, have " +
                                         std::to_string(workspace_bytes));
 
-  order_for_dispatch(items, primary_kind, num_cus);
+  order_for_dispatch(items, num_cus);
   hipStream_t s = as_stream(stream);
   uint8_t* ws = static_cast<uint8_t*>(workspace);
   if (!items.empty()) {

@@ -42,13 +42,10 @@ int waves_per_block_for(int hkv, int64_t items, int64_t num_cus) {
   return w;
 }
 
-void order_for_dispatch(std::vector<WorkItem>& items, int32_t primary_kind, int32_t num_cus) {
+void order_for_dispatch(std::vector<WorkItem>& items, int32_t num_cus) {
   const int64_t cus = num_cus > 0 ? num_cus : 256;
   if (static_cast<int64_t>(items.size()) <= cus) return;
-  auto weight = [primary_kind](const WorkItem& it) {
-    const int pages = it.page_end - it.page_begin;
-    return it.kind == PG_KV_FP16 && primary_kind == PG_KV_INT8 ? 2 * pages : pages;
-  };
+  auto weight = [](const WorkItem& it) { return (it.page_end - it.page_begin) * it.page_weight; };
   std::stable_sort(items.begin(), items.end(), [&](const WorkItem& a, const WorkItem& b) {
     return weight(a) > weight(b);
   });
@@ -252,7 +249,7 @@ int32_t build_plan(const int32_t* host_indptr, const int32_t* host_last_page_len
         const int size = n / c + (k < n % c ? 1 : 0);
         items.push_back(WorkItem{b, sg.kind, sg.seg, start, start + size, sg.last,
                                  static_cast<int32_t>(items.size()) - item_ptr[b], 0, sg.first,
-                                 {0, 0, 0}});
+                                 static_cast<int32_t>(sg.weight), {0, 0}});
         start += size;
         if (sg.seg == 0) split_pages = std::max(split_pages, size);
         else tail_split_pages = std::max(tail_split_pages, size);

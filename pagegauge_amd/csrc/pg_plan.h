@@ -46,7 +46,8 @@ struct WorkItem {
   int32_t item_in_request;  // position of this item among its request's items
   int32_t items_in_request; // number of items of the request
   int32_t request_page_begin;  // absolute index of the request's first page in the segment
-  int32_t reserved[3];
+  int32_t page_weight;  // the planner's weight per page: 2 for FP16 pages planned beside INT8 ones
+  int32_t reserved[2];
 };
 static_assert(sizeof(WorkItem) == 48, "work item layout");
 
@@ -74,6 +75,7 @@ constexpr WorkItem closed_form_item(int i, int items, int tail_items, int tail_b
   it.item_in_request = i;
   it.items_in_request = items;
   it.request_page_begin = base;
+  it.page_weight = tail && primary_kind == PG_KV_INT8 ? 2 : 1;
   return it;
 }
 
@@ -93,11 +95,13 @@ int32_t build_plan(const int32_t* host_indptr, const int32_t* host_last_page_len
                    pg_decode_plan_t& p);
 
 // Device dispatch order of a plan's items: with more items than CUs
-// (several rounds of workgroups), the heaviest items first (FP16 pages
-// weigh twice INT8 pages when the primary segment is INT8), so that the last
-// round holds the lightest ones.  Stable; an item's partial row comes from
-// its request and item_in_request, not from its position, so any order gives
-// the same results.  The host-visible work list stays in request order.
-void order_for_dispatch(std::vector<WorkItem>& items, int32_t primary_kind, int32_t num_cus);
+// (several rounds of workgroups), the heaviest items first, by the weight
+// the planner gave them (pages x page_weight: FP16 pages, the tail's or a
+// heterogeneous table's hinted exact pages, weigh twice INT8 pages), so that
+// the last round holds the lightest ones.  Stable; an item's partial row
+// comes from its request and item_in_request, not from its position, so any
+// order gives the same results.  The host-visible work list stays in request
+// order.
+void order_for_dispatch(std::vector<WorkItem>& items, int32_t num_cus);
 
 }  // namespace pg

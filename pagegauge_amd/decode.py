@@ -183,8 +183,8 @@ class _Planned:
 
 
 WORK_ITEM_FIELDS = ("request", "kind", "segment", "page_begin", "page_end", "last_page",
-                    "item_in_request", "items_in_request", "request_page_begin", "reserved0",
-                    "reserved1", "reserved2")
+                    "item_in_request", "items_in_request", "request_page_begin", "page_weight",
+                    "reserved0", "reserved1")
 
 
 def plan_work_items(indptr, last_page_len, tail_indptr=None, tail_last_page_len=None,

@@ -186,10 +186,21 @@ int main(int argc, char** argv) {
     std::vector<pg::WorkItem> order(n_items);
     if (n_items > 0) std::memcpy(order.data(), raw.data(), n_items * sizeof(pg::WorkItem));
     const std::vector<pg::WorkItem> listed = order;
-    pg::order_for_dispatch(order, kind, cus);
+    pg::order_for_dispatch(order, cus);
+    // the weight the planner gave each item, derived here from the tables:
+    // FP16 tail pages beside INT8 ones, and a hinted table's last pages, x2
     auto weight = [&](const pg::WorkItem& it) {
-      return (it.page_end - it.page_begin) * (it.kind == PG_KV_FP16 && kind == PG_KV_INT8 ? 2 : 1);
+      int per_page = 1;
+      if (it.segment == 1 && kind == PG_KV_INT8) per_page = 2;
+      if (it.segment == 0 && hint > 0) {
+        const int end = indptr[it.request + 1];
+        if (it.page_begin >= end - std::min(hint, end - indptr[it.request])) per_page = 2;
+      }
+      return (it.page_end - it.page_begin) * per_page;
     };
+    for (int i = 0; i < n_items; ++i)
+      check(order[i].page_weight * (order[i].page_end - order[i].page_begin) == weight(order[i]),
+            "an item carries the weight it was planned with", iter);
     if (n_items <= cus) {
       check(n_items == 0 || std::memcmp(order.data(), listed.data(),
                                         n_items * sizeof(pg::WorkItem)) == 0,

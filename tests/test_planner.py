@@ -134,7 +134,7 @@ def _closed_form_items(plan, kind):
         q, r = divmod(n, c)
         begin = base + k * q + min(k, r)
         rows.append([0, 1 if tail else kind, int(tail), begin, begin + q + (k < r), base + n - 1,
-                     i, plan.num_items, base, 0, 0, 0])
+                     i, plan.num_items, base, 2 if tail and kind == 0 else 1, 0, 0])
     return rows
 
 
