@@ -84,3 +84,44 @@ def test_noalloc_centers_check_their_pointers(cuda):
     rc = _capi.library().pg_token_major_centers_noalloc(None, 1024, None, 1024, 16, 8, None, None,
                                                          _stream())
     assert rc == 1 and "null tensor pointer" in _capi.last_error()
+
+
+def test_noalloc_centers_replay_in_a_graph(cuda):
+    """The caller this entry point is for: code under HIP graph capture.  One
+    eager call first (it resolves this GPU's scratch address outside the
+    capture), then the call captured on a side stream and replayed three
+    times, each time after new K/V were copied into the captured buffers and
+    with eager work (the workspace entry point on the same inputs) between
+    the replays; every replay equals the workspace entry point bit for bit."""
+    lib = _capi.library()
+    tokens, heads = 4096 + 13, 8
+    k, v, row = _inputs(tokens, heads, 11, cuda)
+    kc = torch.full((heads, 128), float("nan"), dtype=torch.float16, device=cuda)
+    vc = torch.full_like(kc, float("nan"))
+
+    def call(stream):
+        return lib.pg_token_major_centers_noalloc(k.data_ptr(), row, v.data_ptr(), row, tokens,
+                                                  heads, kc.data_ptr(), vc.data_ptr(), stream)
+
+    assert call(_stream()) == 0, _capi.last_error()          # warm-up, eager
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.graph(graph, stream=side):
+        rc = call(torch.cuda.current_stream().cuda_stream)
+    assert rc == 0, _capi.last_error()
+    torch.cuda.synchronize()
+    for replay in range(3):
+        nk, nv, _ = _inputs(tokens, heads, 100 + replay, cuda)
+        k.copy_(nk)
+        v.copy_(nv)
+        kc.fill_(float("nan"))
+        vc.fill_(float("nan"))
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        want_k, want_v = _with_workspace(k, v, row, tokens, heads)   # eager work between replays
+        torch.cuda.synchronize()
+        assert torch.equal(kc.view(torch.int16), want_k.view(torch.int16)), replay
+        assert torch.equal(vc.view(torch.int16), want_v.view(torch.int16)), replay
