@@ -97,6 +97,15 @@ def parse_args() -> argparse.Namespace:
     p.add_argument("--pmc-calls", type=int, default=0,
                    help="counter-collection driver for rocprofv3 --pmc: N cold decode calls, "
                         "then N plain 64 MiB copies of known size; prints one JSON line, no timing")
+    p.add_argument("--freeze-splits", default="",
+                   help="with --pilot: write the per-shape, per-method argmin splits to this JSON "
+                        "file (the reference's FROZEN_SELECTION.json)")
+    p.add_argument("--frozen-splits", default="",
+                   help="a --freeze-splits file: the validation-seed study plans INT8 and FP16 "
+                        "with their frozen B1/49K splits instead of the planner")
+    p.add_argument("--pmc-fp16", action="store_true",
+                   help="the --pmc-calls driver runs the FP16 same-way call instead of the INT8 "
+                        "one (same workload, an FP16 copy of every page)")
     return p.parse_args()
 
 
@@ -935,13 +944,20 @@ def bootstrap_median_ci(values, samples: int = 20000, seed: int = BOOTSTRAP_SEED
     return [round(_quantile(medians, 0.025), 4), round(_quantile(medians, 0.975), 4)]
 
 
-def seed_study(torch, decode, workloads, device, seeds, scrub, overhead, repeats: int = 20):
+def seed_study(torch, decode, workloads, device, seeds, scrub, overhead, repeats: int = 20,
+               frozen=None):
     """B1/49K over the validation seeds (scripts/run_page_gauge_validation.py:47-52):
     per seed, the paired INT8-vs-FP16 same-way protocol (cache-neutral after
     the reference's 256 MiB scrub, cache-hot), the attention-only speedup
     and the inclusive one (INT8 attention p50 + the fused-append increment
     per step, scripts/summarize_page_gauge_results.py:105-115); then the
-    median over seeds and its 95 % bootstrap interval."""
+    median over seeds and its 95 % bootstrap interval.  ``frozen``: a
+    selection written by ``--pilot --freeze-splits``; each method then uses
+    its frozen B1/49K split (0 = the planner), as the reference reuses its
+    pilot's argmin for the validation seeds (:376-416)."""
+    split = {"int8": 0, "fp16": 0}
+    if frozen is not None:
+        split = {m: int(frozen["shapes"]["b1_49k"][m]) for m in ("int8", "fp16")}
     per_seed = []
     for seed in seeds:
         w = workloads.b1_49k(seed, device=device, with_fp16_copy=True)
@@ -949,13 +965,13 @@ def seed_study(torch, decode, workloads, device, seeds, scrub, overhead, repeats
         lse = torch.empty(w.batch, 32, dtype=torch.float32, device=device)
         seg = decode.PageGaugeSegmentedDecode(torch.empty(64 << 20, dtype=torch.uint8, device=device))
         seg.plan(w.old_indptr, w.old_indices, w.old_last_page_len, w.tail_indptr, w.tail_indices,
-                 w.tail_last_page_len)
+                 w.tail_last_page_len, fixed_split_size=split["int8"] or None)
         int8 = seg.bind(w.query, (w.k_codes, w.v_codes), w.k_scale, w.v_scale, (w.tail_k, w.tail_v),
                         w.value_center, out=out, lse=lse)
         f16 = decode.BatchDecodeWithPagedKVCacheWrapper(
             torch.empty(64 << 20, dtype=torch.uint8, device=device), "NHD")
         f16.plan(w.fp16_indptr, w.fp16_indices, w.fp16_last_page_len, 32, 8, 128, 16,
-                 kv_data_type=torch.float16)
+                 kv_data_type=torch.float16, fixed_split_size=split["fp16"] or None)
         fp16 = f16.bind(w.query, (w.fp16_k, w.fp16_v), out=torch.empty_like(out),
                         lse=torch.empty_like(lse))
         pair = controlled_pair(torch, {"page_gauge_int8": int8, "fp16_same_way": fp16}, 3,
@@ -972,7 +988,9 @@ def seed_study(torch, decode, workloads, device, seeds, scrub, overhead, repeats
         del w, seg, f16, int8, fp16
         torch.cuda.empty_cache()
     summary = {"seeds": list(seeds), "per_seed": per_seed,
-               "append_increment_source": "append_overhead (B=1, paired, 16-step cycles)"}
+               "append_increment_source": "append_overhead (B=1, paired, 16-step cycles)",
+               "splits": {m: (v or "planner") for m, v in split.items()},
+               "split_source": frozen.get("source") if frozen is not None else "the planner"}
     for mode in ("cache_neutral", "cache_hot"):
         # the reference resamples the inclusive ratios with the next seed
         # (scripts/summarize_page_gauge_results.py:56-69)
@@ -1258,6 +1276,23 @@ def phase_trace(torch, decode, workloads, device, scrub, calls: int):
 PILOT_SPLITS = (0, 8, 16, 28, 48, 64)
 
 
+def frozen_selection(pilot: dict) -> dict:
+    """The reference's FROZEN_SELECTION.json of a pilot sweep
+    (scripts/run_page_gauge_validation.py:295-316, :398-418): per shape and
+    method the argmin split of the cold call p50 (0 = the planner)."""
+    shapes = {}
+    for name, row in pilot.items():
+        if isinstance(row, dict) and "int8" in row:
+            shapes[name] = {m: int(row[m]["argmin"]) for m in ("int8", "fp16")}
+            shapes[name]["rows"] = {m: {k: v["call_p50_us"] for k, v in row[m].items()
+                                        if isinstance(v, dict)} for m in ("int8", "fp16")}
+    return {"source": f"pilot sweep, seed {PILOT_SEED_NOTE}, cold (clean 1 GiB read scrub)",
+            "selection_timing_mode": "cache_neutral", "shapes": shapes}
+
+
+PILOT_SEED_NOTE = "20260814 (B1 shapes) / the validation seeds (B8 ragged)"
+
+
 def pilot_sweep(torch, decode, workloads, device, scrub, samples: int = 30):
     """The reference's pilot sweep (scripts/run_page_gauge_validation.py:277-297,
     :376-416): for each method (INT8 PageGauge, FP16 same-way) every split
@@ -1381,11 +1416,26 @@ def main() -> int:
     scrub_clean = lambda: torch.amax(scrub_clean_buf, dim=0, out=scrub_sink)  # noqa: E731
 
     if args.pmc_calls:
-        print(json.dumps({**pmc_driver(torch, bound, args.pmc_calls, scrub_clean, device),
+        driven, what = bound, "int8"
+        if args.pmc_fp16:
+            if w.fp16_k is None:
+                raise SystemExit("--pmc-fp16 needs the FP16 copy (drop --no-fp16)")
+            wrap16 = decode.BatchDecodeWithPagedKVCacheWrapper(
+                torch.empty(64 << 20, dtype=torch.uint8, device=device), "NHD")
+            wrap16.plan(w.fp16_indptr, w.fp16_indices, w.fp16_last_page_len, 32, 8, 128, 16,
+                        kv_data_type=torch.float16)
+            driven = wrap16.bind(w.query, (w.fp16_k, w.fp16_v), out=torch.empty_like(w.query),
+                                 lse=torch.empty_like(lse))
+            what = "fp16_same_way"
+        print(json.dumps({**pmc_driver(torch, driven, args.pmc_calls, scrub_clean, device),
+                          "call": what, "workload": args.workload,
                           "library_variant": args.library_variant}), flush=True)
         return 0
     if args.pilot:
-        print(json.dumps(pilot_sweep(torch, decode, workloads, device, scrub_clean)), flush=True)
+        pilot = pilot_sweep(torch, decode, workloads, device, scrub_clean)
+        if args.freeze_splits:
+            Path(args.freeze_splits).write_text(json.dumps(frozen_selection(pilot), indent=1) + "\n")
+        print(json.dumps(pilot), flush=True)
         return 0
     if args.stream_probe:
         result = {"b1_49k": stream_probe(torch, w, bound, scrub_clean)}
@@ -1496,6 +1546,11 @@ def main() -> int:
         other = {"config1_b1_4k": decode_config(
             torch, decode, workloads.single_4k(args.seed, device=device, with_fp16_copy=True),
             scrub_clean, 30)}
+        # config 5's per-layer decode shape: 16K context (1008 INT8 pages + the ring)
+        other["b1_16k"] = decode_config(
+            torch, decode, workloads.build_decode_workload([16384 + 16], args.seed, device=device,
+                                                           with_fp16_copy=True), scrub_clean, 30)
+        torch.cuda.empty_cache()
         # B1/49K through the heterogeneous one-table decode (same pages)
         out_h = torch.empty_like(w.query)
         het = heterogeneous_call(torch, decode, w, device, out_h)
@@ -1541,8 +1596,10 @@ def main() -> int:
     overhead = append_overhead(torch, device, scrub_rmw)
     seeds = None
     if args.seeds > 0 and not args.no_fp16:
+        frozen = json.loads(Path(args.frozen_splits).read_text()) if args.frozen_splits else None
         seeds = seed_study(torch, decode, workloads, device,
-                           workloads.VALIDATION_SEEDS[:args.seeds], scrub_rmw, overhead)
+                           workloads.VALIDATION_SEEDS[:args.seeds], scrub_rmw, overhead,
+                           frozen=frozen)
 
     cpu = None
     parity = None

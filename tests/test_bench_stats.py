@@ -60,3 +60,51 @@ def test_more_than_one_gpu_is_refused(monkeypatch, capsys):
     monkeypatch.setattr("sys.argv", ["bench.py", "--gpus", "2"])
     assert bench.main() == 2
     assert "one GPU" in capsys.readouterr().err
+
+
+def test_frozen_selection_takes_each_methods_argmin():
+    """--pilot --freeze-splits: per shape and method the argmin split of the
+    pilot's cold call p50 (the reference's FROZEN_SELECTION.json)."""
+    pilot = {"splits": [0, 8, 28], "state": "cold",
+             "b1_49k": {"lengths": [49152],
+                        "int8": {"0": {"call_p50_us": 27.1, "items": 112},
+                                 "8": {"call_p50_us": 30.0, "items": 384},
+                                 "28": {"call_p50_us": 26.9, "items": 112},
+                                 "argmin": "28", "planner_over_argmin": 1.007},
+                        "fp16": {"0": {"call_p50_us": 42.0, "items": 112},
+                                 "8": {"call_p50_us": 50.0, "items": 384},
+                                 "28": {"call_p50_us": 44.0, "items": 112},
+                                 "argmin": "0", "planner_over_argmin": 1.0}}}
+    frozen = bench.frozen_selection(pilot)
+    assert frozen["shapes"]["b1_49k"]["int8"] == 28
+    assert frozen["shapes"]["b1_49k"]["fp16"] == 0
+    assert frozen["shapes"]["b1_49k"]["rows"]["int8"] == {"0": 27.1, "8": 30.0, "28": 26.9}
+    assert frozen["selection_timing_mode"] == "cache_neutral"
+
+
+def test_trace_summary_phases_per_xcd():
+    """bench.py --trace's arithmetic on two hand-made rows: one INT8 wave per
+    XCD whose clocks differ by 1000 ticks (times are taken per XCD), two
+    4-page groups, and the 32-bit wrap of s_memrealtime."""
+    rows = np.zeros((2, 64), dtype=np.int64)
+    for w, (xcc, base) in enumerate(((0, 2 ** 32 - 50), (1, 1000))):
+        r = rows[w]
+        r[bench.TRACE_XCC], r[bench.TRACE_KIND], r[bench.TRACE_PAGES] = xcc, 0, 8
+        marks = {bench.TRACE_START: 0, bench.TRACE_IDS: 150, bench.TRACE_ISSUED: 270,
+                 bench.TRACE_K: 530, bench.TRACE_V: 580, bench.TRACE_DONE: 600,
+                 bench.TRACE_K + 1: 700, bench.TRACE_V + 1: 750, bench.TRACE_DONE + 1: 770,
+                 bench.TRACE_END: 800}
+        for lane, t in marks.items():
+            r[lane] = (base + t) % 2 ** 32
+    out = bench.trace_summary([rows.astype(np.uint32).view(np.int32)], [9.0])
+    tick = bench.TRACE_TICK_US
+    assert out["start_at"]["max"] == 0.0                       # per XCD, not across
+    assert out["ids_rtt"]["p50"] == pytest.approx(150 * tick)
+    assert out["first_k_after_issue"]["p50"] == pytest.approx(260 * tick)
+    assert out["k_wait"]["p50"] == pytest.approx(100 * tick)   # K[1] - done[0]
+    assert out["qk_to_v"]["p50"] == pytest.approx(50 * tick)
+    assert out["pv"]["p50"] == pytest.approx(20 * tick)
+    assert out["group_span"]["p50"] == pytest.approx(170 * tick)
+    assert out["end_at"]["max"] == pytest.approx(800 * tick)
+    assert out["end_at_p50_by_xcc"] == {0: 8.0, 1: 8.0}
+    assert out["waves_per_call"] == 2 and out["kernel_event_mean_us"] == 9.0
