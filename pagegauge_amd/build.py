@@ -20,7 +20,9 @@ digest of the sources and flags it was built from (``variant_is_current``):
 * ``trace``: the product with the partial kernel's per-wave phase trace
   compiled in (``-DPG_TRACE=1``, ``pg_trace_set_buffer``; bench.py --trace);
 * ``trace_conditional_scales``: the trace build with the page-scale loads in
-  their earlier conditional form (bench.py --trace's before/after).
+  their earlier conditional form (bench.py --trace's before/after);
+* ``default_scheduler``: the product with the decode source under LLVM's
+  default machine scheduler instead of the memory-clause strategy.
 """
 
 from __future__ import annotations
@@ -56,7 +58,8 @@ SOURCES = {
     "pg_plan.cpp": [],
     "pg_update.hip": ["-ffp-contract=off"],
     # the memory-clause scheduler keeps the partial kernel's page-group loads
-    # together: measured 1-3 % faster (B1/49K, 16K, B8 ragged), same bits
+    # together: about 1 % faster from 16K tokens up (the default_scheduler
+    # variant against it), same output bits
     "pg_decode.hip": ["-mllvm", "-amdgpu-sched-strategy=max-memory-clause"],
     "pg_decoder.hip": [],
 }
@@ -71,6 +74,8 @@ VARIANTS = {
     "trace": {"pg_decode.hip": ["-DPG_TRACE=1"]},
     "trace_conditional_scales": {"pg_decode.hip": ["-DPG_TRACE=1",
                                                    "-DPG_CONDITIONAL_SCALE_LOADS=1"]},
+    # None: the source's own flags are dropped, not extended
+    "default_scheduler": {"pg_decode.hip": None},
 }
 
 
@@ -136,7 +141,7 @@ def variant_sources(variant: str) -> dict:
         raise ValueError(f"unknown variant {variant!r}; known: {sorted(VARIANTS)}")
     sources = dict(SOURCES)
     for source, flags in VARIANTS[variant].items():
-        sources[source] = sources[source] + flags
+        sources[source] = [] if flags is None else sources[source] + flags
     return sources
 
 
