@@ -90,6 +90,9 @@ def parse_args() -> argparse.Namespace:
                         "trace_conditional_scales): the variant name; B1/49K, 16K and 4K, "
                         "cold calls; prints one JSON line")
     p.add_argument("--trace-calls", type=int, default=20)
+    p.add_argument("--trace-dump", default="",
+                   help="with --trace: also save every traced call's raw rows (partial and "
+                        "combine kernels) to this .npz file, one array per workload")
     p.add_argument("--workload", choices=("b1_49k", "b1_16k", "config1", "serving_b256"),
                    default="b1_49k",
                    help="workload of the --pmc-calls driver (config1: B=1, 4096 tokens; "
@@ -1158,6 +1161,9 @@ TRACE_START, TRACE_IDS, TRACE_ISSUED, TRACE_SCALES = 0, 1, 2, 3
 TRACE_K, TRACE_V, TRACE_DONE, TRACE_END = 4, 20, 36, 52
 TRACE_XCC, TRACE_HWID, TRACE_ITEM, TRACE_KIND, TRACE_PAGES = 53, 54, 55, 56, 57
 TRACE_TICK_US = 0.01
+# combine kernel rows (written after the partial kernel's rows)
+CTRACE_META, CTRACE_ROWS, CTRACE_MAX, CTRACE_SUMS, CTRACE_END = 1, 2, 3, 4, 5
+CTRACE_KIND = 100
 
 
 def _trace_stats(values):
@@ -1225,7 +1231,45 @@ def trace_summary(rows_per_call, kernel_us):
     return out
 
 
-def phase_trace(torch, decode, workloads, device, scrub, calls: int):
+def combine_trace_summary(partial_per_call, combine_per_call):
+    """Phase statistics (µs) of the combine kernel's trace rows.
+
+    Per XCD, times are relative to the first partial-kernel wave start on
+    that XCD (the counters of one XCD agree with each other): the kernel
+    boundary is the first combine wave start minus the last partial wave
+    end, both on the same XCD.  Per combine wave: value center and item
+    range arrival, partial rows arrival, the maximum over the rows, the sums
+    (rows whose sums mark is unset are skipped), end."""
+    import numpy as np
+    agg = {k: [] for k in ("boundary", "start_spread", "meta_rtt", "rows_rtt", "max_after_rows",
+                           "sums_after_max", "end_after_sums", "wave_life", "span")}
+    for rp, rc in zip(partial_per_call, combine_per_call):
+        p = rp.astype(np.int64) & 0xFFFFFFFF
+        c = rc.astype(np.int64) & 0xFFFFFFFF
+        if not np.all(c[:, TRACE_KIND] == CTRACE_KIND):
+            raise RuntimeError("combine trace rows missing: is the buffer sized for both kernels?")
+        pxcc, cxcc = p[:, TRACE_XCC] & 0xF, c[:, TRACE_XCC] & 0xF
+        for x in np.unique(cxcc):
+            pp, cc = p[pxcc == x], c[cxcc == x]
+            if len(pp) == 0:
+                continue
+            t0 = pp[:, TRACE_START].min()
+            rel = lambda rows, col: ((rows[:, col] - t0) & 0xFFFFFFFF) * TRACE_TICK_US  # noqa: E731
+            start = rel(cc, TRACE_START)
+            agg["boundary"].append(float(start.min() - rel(pp, TRACE_END).max()))
+            agg["start_spread"] += list(start - start.min())
+            agg["meta_rtt"] += list(rel(cc, CTRACE_META) - start)
+            agg["rows_rtt"] += list(rel(cc, CTRACE_ROWS) - start)
+            agg["max_after_rows"] += list(rel(cc, CTRACE_MAX) - rel(cc, CTRACE_ROWS))
+            w0 = cc[:, CTRACE_SUMS] != 0
+            agg["sums_after_max"] += list((rel(cc, CTRACE_SUMS) - rel(cc, CTRACE_MAX))[w0])
+            agg["end_after_sums"] += list((rel(cc, CTRACE_END) - rel(cc, CTRACE_SUMS))[w0])
+            agg["wave_life"] += list(rel(cc, CTRACE_END) - start)
+            agg["span"].append(float(rel(cc, CTRACE_END).max() - start.min()))
+    return {k: _trace_stats(v) for k, v in agg.items()}
+
+
+def phase_trace(torch, decode, workloads, device, scrub, calls: int, dump: str = ""):
     """Per-wave phase trace of the partial kernel (trace build loaded), cold
     calls after the clean scrub, at B1/49K, 16K and 4K."""
     from pagegauge_amd import _capi
@@ -1233,7 +1277,7 @@ def phase_trace(torch, decode, workloads, device, scrub, calls: int):
     lib = _capi.library()
     if not hasattr(lib, "pg_trace_set_buffer"):
         raise RuntimeError("--trace needs a trace build (python -m pagegauge_amd.build --variant trace)")
-    result = {}
+    result, raw = {}, {}
     cases = (("b1_49k", lambda: workloads.b1_49k(workloads.VALIDATION_SEEDS[0], device=device)),
              ("b1_16k", lambda: workloads.build_decode_workload([16384 + 16], workloads.VALIDATION_SEEDS[0],
                                                                 device=device)),
@@ -1247,12 +1291,13 @@ def phase_trace(torch, decode, workloads, device, scrub, calls: int):
                          w.value_center, out=torch.empty_like(w.query),
                          lse=torch.empty(w.batch, 32, dtype=torch.float32, device=device))
         waves = dec.num_work_items * 8
-        buf = torch.zeros(waves * 64, dtype=torch.int32, device=device)
+        combine_waves = w.batch * 32 * 4 * 4      # (request, query head) x 4 quarters x 4 waves
+        buf = torch.zeros((waves + combine_waves) * 64, dtype=torch.int32, device=device)
         _capi.check(lib.pg_trace_set_buffer(buf.data_ptr(), buf.numel() * 4), "trace")
         for _ in range(3):
             scrub()
             bound()
-        rows, kernel = [], []
+        rows, combine_rows, kernel = [], [], []
         for _ in range(calls):
             start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
             start.record()
@@ -1263,13 +1308,24 @@ def phase_trace(torch, decode, workloads, device, scrub, calls: int):
             bound.combine()
             torch.cuda.synchronize()
             kernel.append(1e3 * start.elapsed_time(stop))
-            rows.append(buf.view(waves, 64).cpu().numpy().copy())
+            host = buf.view(waves + combine_waves, 64).cpu().numpy()
+            rows.append(host[:waves].copy())
+            combine_rows.append(host[waves:].copy())
         _capi.check(lib.pg_trace_set_buffer(None, 0), "trace")
+        if dump:
+            import numpy as np
+            raw[f"{name}_partial"] = np.stack(rows)
+            raw[f"{name}_combine"] = np.stack(combine_rows)
+            raw[f"{name}_kernel_us"] = np.asarray(kernel)
         result[name] = {"work_items": dec.num_work_items,
                         "waves_per_block": int(dec._state.plan.waves_per_block),
-                        **trace_summary(rows, kernel)}
+                        **trace_summary(rows, kernel),
+                        "combine": combine_trace_summary(rows, combine_rows)}
         del w, dec, bound, buf
         torch.cuda.empty_cache()
+    if dump:
+        import numpy as np
+        np.savez_compressed(dump, **raw)
     return result
 
 
@@ -1377,7 +1433,7 @@ def main() -> int:
         sink = torch.empty((), dtype=torch.int32, device=device)
         print(json.dumps({"trace_build": args.trace, **phase_trace(
             torch, decode, workloads, device, lambda: torch.amax(buf, dim=0, out=sink),
-            args.trace_calls)}), flush=True)
+            args.trace_calls, args.trace_dump)}), flush=True)
         return 0
     if args.paper_only:
         buf = torch.ones((args.big_scrub_mib << 20) // 4, dtype=torch.int32, device=device)

@@ -22,7 +22,9 @@ digest of the sources and flags it was built from (``variant_is_current``):
 * ``trace_conditional_scales``: the trace build with the page-scale loads in
   their earlier conditional form (bench.py --trace's before/after);
 * ``default_scheduler``: the product with the decode source under LLVM's
-  default machine scheduler instead of the memory-clause strategy.
+  default machine scheduler instead of the memory-clause strategy;
+* ``interleaved_heads``: the KV heads of an item's two workgroups
+  interleaved (even, odd) instead of in blocks (0-3, 4-7).
 """
 
 from __future__ import annotations
@@ -76,6 +78,7 @@ VARIANTS = {
                                                    "-DPG_CONDITIONAL_SCALE_LOADS=1"]},
     # None: the source's own flags are dropped, not extended
     "default_scheduler": {"pg_decode.hip": None},
+    "interleaved_heads": {"pg_decode.hip": ["-DPG_INTERLEAVED_HEADS=1"]},
 }
 
 

@@ -94,11 +94,25 @@ constexpr int kTraceItem = 55;      // (blockIdx.x << 8) | kv head
 constexpr int kTraceKind = 56;      // work item kind
 constexpr int kTracePages = 57;     // pages of the chunk
 constexpr int kTraceSlots = 16;     // traced groups (FP16 pages) per wave
+// The combine kernel's waves write rows of the same shape after the partial
+// kernel's rows (lanes 53-55 as above, lane 56 = kTraceCombineKind):
+constexpr int kCTraceMeta = 1;      // value-center bits and the item range arrived
+constexpr int kCTraceRows = 2;      // the partial rows (o, m, l) arrived
+constexpr int kCTraceMax = 3;       // the block's maximum read back after its barrier
+constexpr int kCTraceSums = 4;      // the block's sums read back after their barrier
+constexpr int kCTraceEnd = 5;       // outputs stored
+constexpr uint32_t kTraceCombineKind = 100;
 // Alternative build for the trace's before/after only: the page-scale loads
 // in the conditional form the kernel had before (each compiled to a branch
 // that waits for its load before the next one leaves).
 #ifndef PG_CONDITIONAL_SCALE_LOADS
 #define PG_CONDITIONAL_SCALE_LOADS 0
+#endif
+// Alternative build for the A/B only: the KV heads of an item's workgroups
+// interleaved (workgroup y of Y takes heads y, y + Y, ...) instead of in
+// blocks.
+#ifndef PG_INTERLEAVED_HEADS
+#define PG_INTERLEAVED_HEADS 0
 #endif
 
 struct DecodeArgs {
@@ -159,18 +173,19 @@ struct HeadState {
 };
 
 #if PG_TRACE
-__device__ __forceinline__ void trace_put(HeadState& st, int slot, uint32_t value) {
-  st.trace = static_cast<int>(threadIdx.x % kWave) == slot ? value : st.trace;
+// ``word``: the wave's trace register (lane i holds trace word i)
+__device__ __forceinline__ void trace_put(uint32_t& word, int slot, uint32_t value) {
+  word = static_cast<int>(threadIdx.x % kWave) == slot ? value : word;
 }
-__device__ __forceinline__ void trace_mark(HeadState& st, int slot) {
+__device__ __forceinline__ void trace_mark(uint32_t& word, int slot) {
   uint64_t t;
   asm volatile("s_memrealtime %0\n\ts_waitcnt lgkmcnt(0)" : "=s"(t) : : "memory");
-  trace_put(st, slot, static_cast<uint32_t>(t));
+  trace_put(word, slot, static_cast<uint32_t>(t));
 }
-__device__ __forceinline__ void trace_mark_after(HeadState& st, int slot, uint32_t loaded) {
+__device__ __forceinline__ void trace_mark_after(uint32_t& word, int slot, uint32_t loaded) {
   uint64_t t;
   asm volatile("s_memrealtime %0\n\ts_waitcnt lgkmcnt(0)" : "=s"(t) : "v"(loaded) : "memory");
-  trace_put(st, slot, static_cast<uint32_t>(t));
+  trace_put(word, slot, static_cast<uint32_t>(t));
 }
 __device__ __forceinline__ uint32_t trace_hwreg_xcc() {
   uint32_t x;
@@ -182,9 +197,9 @@ __device__ __forceinline__ uint32_t trace_hwreg_id() {
   asm volatile("s_getreg_b32 %0, hwreg(HW_REG_HW_ID)" : "=s"(x));
   return x;
 }
-#define PG_TRACE_MARK(st, slot) trace_mark((st), (slot))
-#define PG_TRACE_AFTER(st, slot, loaded) trace_mark_after((st), (slot), static_cast<uint32_t>(loaded))
-#define PG_TRACE_PUT(st, slot, value) trace_put((st), (slot), static_cast<uint32_t>(value))
+#define PG_TRACE_MARK(st, slot) trace_mark((st).trace, (slot))
+#define PG_TRACE_AFTER(st, slot, loaded) trace_mark_after((st).trace, (slot), static_cast<uint32_t>(loaded))
+#define PG_TRACE_PUT(st, slot, value) trace_put((st).trace, (slot), static_cast<uint32_t>(value))
 #else
 #define PG_TRACE_MARK(st, slot) ((void)0)
 #define PG_TRACE_AFTER(st, slot, loaded) ((void)0)
@@ -829,6 +844,9 @@ struct CombineArgs {
   int num_qo_heads;
   int max_items;
   int uniform_items;   // > 0: every request has this many items (no item_ptr read)
+#if PG_TRACE
+  uint32_t* trace;     // [waves of the combine grid][64] words, or null
+#endif
 };
 
 __device__ __forceinline__ void fma4(float4& acc, float w, const float4& v) {
@@ -849,40 +867,36 @@ __device__ __forceinline__ float combine_output(float total, float inv, float ce
   return o;
 }
 
-// Shared memory of one combine unit (256 threads).
-struct CombineShared {
-  float wave_max[kCombineThreads / kWave];
-  float4 wave_acc[kCombineThreads / kWave][kCombineCols];
-  float wave_l[kCombineThreads / kWave];
-};
-
 // Merges the partials of (request, query head) for dims 32*quarter.. +31 and
-// writes out/lse.  ``tid`` in [0, 256); every thread of the block calls this
-// the same number of times (it contains block barriers); ``active`` false
-// runs the barriers only.
+// writes out/lse; ``tid`` in [0, 256).  Every wave works alone (no LDS, no
+// barrier): wave w owns float4 columns 2w and 2w + 1.
 //
 // One memory round trip: the partial rows are loaded for the plan's largest
 // item count while the request's own count is loaded; rows past the count
-// are dropped by selects (they may hold anything).  The 16 lanes of a DPP row
-// hold 16 item rows of one float4 column, so the row reductions are DPP
-// rotations within the row plus one LDS exchange between the four waves.
+// are dropped by selects (they may hold anything).  DPP row q of a wave holds
+// column 2w + q/2 and the item rows of half h = q % 2: lane i of the row
+// accumulates rows i + 16h + 32k, k = 0, 1, ... in order, and the row's 16
+// lanes reduce by DPP rotations (the tree that row16_sum forms at lane 0).
+// The two halves of a column sit 16 lanes apart, so the maximum over all
+// rows and the sum of the two half totals take one swap of 16 lanes each.
+// That is the association combine_rows_kernel also keeps: per item w*o (one
+// rounding), the 16-lane tree over each half, then the sum of the halves.
 __device__ __forceinline__ void combine_unit(const CombineArgs& a, int row_head, int quarter,
-                                             int tid, bool active, CombineShared& sh) {
+                                             int tid, uint32_t& trace) {
   const int request = row_head / a.num_qo_heads;
   const int qh = row_head % a.num_qo_heads;
   const int wave = tid / kWave;
   const int lane = tid % kWave;
-  // wave w, DPP row q, lane i of the row: float4 column (w % 2) * 4 + q, item
-  // row i + 16 * (w / 2) (+ 32 k); a column's rows reduce within one DPP row
-  const int c = (wave & 1) * 4 + (lane >> 4);
-  const int r = (lane & 15) + 16 * (wave >> 1);
+  const int q = lane >> 4;
+  const int c = 2 * wave + (q >> 1);
+  const int r = (lane & 15) + 16 * (q & 1);
   const int dim = 32 * quarter + 4 * c;
   const int64_t base = static_cast<int64_t>(row_head) * a.max_items;
   const float* pm = a.partial_m + base;
   const float* pl = a.partial_l + base;
   const float* po = a.partial_o + base * kHeadDim + dim;
 
-  // The value center: every thread loads the 8-byte slice of column tid % 8
+  // The value center: every lane loads the 8-byte slice of its column
   // unconditionally (with no center, the first 8 bytes of this row's
   // partials, whose bits are dropped) and converts it only after the partial
   // rows are requested.  A conditional load compiles to a branch that waits
@@ -890,7 +904,7 @@ __device__ __forceinline__ void combine_unit(const CombineArgs& a, int row_head,
   const bool has_center = a.value_center != nullptr;
   const uint16_t* cv = has_center
                            ? a.value_center + request * a.center_batch_stride +
-                                 (qh / kGqa) * kHeadDim + 32 * quarter + 4 * (tid % kCombineCols)
+                                 (qh / kGqa) * kHeadDim + dim
                            : reinterpret_cast<const uint16_t*>(a.partial_o + base * kHeadDim);
   uint2 center_bits = *reinterpret_cast<const uint2*>(cv);
   // the request's item count, used only after the rows are requested
@@ -901,7 +915,7 @@ __device__ __forceinline__ void combine_unit(const CombineArgs& a, int row_head,
 #pragma unroll
   for (int k = 0; k < kCombineInRegs; ++k) {
     const int j = r + k * kCombineRows;
-    const bool planned = active && j < a.max_items;
+    const bool planned = j < a.max_items;
     ov[k] = planned ? *reinterpret_cast<const float4*>(po + static_cast<int64_t>(j) * kHeadDim)
                     : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
     mv[k] = planned ? pm[j] : kNegInf;
@@ -911,7 +925,13 @@ __device__ __forceinline__ void combine_unit(const CombineArgs& a, int row_head,
   consume_point(center_bits.y);
   consume_point(item_begin);
   consume_point(item_end);
-  const int count = !active ? 0 : a.uniform_items > 0 ? a.uniform_items : item_end - item_begin;
+#if PG_TRACE
+  trace_mark_after(trace, kCTraceMeta, center_bits.y ^ static_cast<uint32_t>(item_end));
+  trace_mark_after(trace, kCTraceRows, __float_as_uint(ov[kCombineInRegs - 1].w));
+  trace_mark_after(trace, kCTraceRows, __float_as_uint(mv[kCombineInRegs - 1]));
+  trace_mark_after(trace, kCTraceRows, __float_as_uint(lv[kCombineInRegs - 1]));
+#endif
+  const int count = a.uniform_items > 0 ? a.uniform_items : item_end - item_begin;
   float center4[4] = {0.0f, 0.0f, 0.0f, 0.0f};
   if (has_center) {
     center4[0] = half_bits_to_float(static_cast<uint16_t>(center_bits.x));
@@ -929,11 +949,11 @@ __device__ __forceinline__ void combine_unit(const CombineArgs& a, int row_head,
   for (int j = r + kCombineInRegs * kCombineRows; j < count; j += kCombineRows)
     local_max = fmaxf(local_max, pm[j]);
   local_max = row16_max(local_max);
-  if (lane == 0) sh.wave_max[wave] = local_max;
-  __syncthreads();
-  float m = sh.wave_max[0];
-#pragma unroll
-  for (int w = 1; w < kCombineThreads / kWave; ++w) m = fmaxf(m, sh.wave_max[w]);
+  // the other half's maximum, 16 lanes away (the maximum is exact in any order)
+  const float m = fmaxf(local_max, __shfl_xor(local_max, 16, kWave));
+#if PG_TRACE
+  trace_mark_after(trace, kCTraceMax, __float_as_uint(m));
+#endif
 
   float4 acc = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
   float lsum = 0.0f;
@@ -957,34 +977,50 @@ __device__ __forceinline__ void combine_unit(const CombineArgs& a, int row_head,
   acc.z = row16_sum(acc.z);
   acc.w = row16_sum(acc.w);
   lsum = row16_sum(lsum);
-  if ((lane & 15) == 0) sh.wave_acc[wave][lane >> 4] = acc;
-  if (lane == 0) sh.wave_l[wave] = lsum;
-  __syncthreads();
-  if (active && tid < kCombineCols) {
-    // column tid: waves tid / 4 (rows 0-15) and 2 + tid / 4 (rows 16-31), DPP row tid % 4
-    const float4 v0 = sh.wave_acc[tid >> 2][tid & 3];
-    const float4 v1 = sh.wave_acc[2 + (tid >> 2)][tid & 3];
-    const float4 total = make_float4(v0.x + v1.x, v0.y + v1.y, v0.z + v1.z, v0.w + v1.w);
-    const float l = sh.wave_l[0] + sh.wave_l[2];
+  // half 0 + half 1 (IEEE addition commutes, so both rows of the pair hold
+  // the same bits); lane 0 of each row holds its 16-lane tree
+  const float4 total = make_float4(acc.x + __shfl_xor(acc.x, 16, kWave),
+                                   acc.y + __shfl_xor(acc.y, 16, kWave),
+                                   acc.z + __shfl_xor(acc.z, 16, kWave),
+                                   acc.w + __shfl_xor(acc.w, 16, kWave));
+  const float l = lsum + __shfl_xor(lsum, 16, kWave);
+#if PG_TRACE
+  trace_mark_after(trace, kCTraceSums, __float_as_uint(l) ^ __float_as_uint(total.x));
+#endif
+  if ((lane & 31) == 0) {
+    // lane 0 of DPP row 0 (column 2w) and of row 2 (column 2w + 1)
     const bool empty = !(l > 0.0f);
     const float inv = empty ? 0.0f : 1.0f / l;
     const float o4[4] = {combine_output(total.x, inv, center4[0]),
                          combine_output(total.y, inv, center4[1]),
                          combine_output(total.z, inv, center4[2]),
                          combine_output(total.w, inv, center4[3])};
-    const int d = 32 * quarter + 4 * tid;
-    uint16_t* out = a.out + static_cast<int64_t>(row_head) * kHeadDim + d;
+    uint16_t* out = a.out + static_cast<int64_t>(row_head) * kHeadDim + dim;
     *reinterpret_cast<__half2*>(out) = __floats2half2_rn(o4[0], o4[1]);
     *reinterpret_cast<__half2*>(out + 2) = __floats2half2_rn(o4[2], o4[3]);
     if (tid == 0 && quarter == 0 && a.lse != nullptr)
       a.lse[row_head] = empty ? kNegInf : log2f(l) + m;
   }
-  __syncthreads();   // the shared buffers are reused by the next unit
 }
 
 __global__ __launch_bounds__(kCombineThreads) void combine_kernel(CombineArgs a) {
-  __shared__ CombineShared sh;
-  combine_unit(a, blockIdx.x, blockIdx.y, threadIdx.x, true, sh);
+  uint32_t trace = 0;
+#if PG_TRACE
+  trace_mark(trace, kTraceStart);
+#endif
+  combine_unit(a, blockIdx.x, blockIdx.y, threadIdx.x, trace);
+#if PG_TRACE
+  if (a.trace != nullptr) {
+    trace_mark(trace, kCTraceEnd);
+    trace_put(trace, kTraceXcc, trace_hwreg_xcc());
+    trace_put(trace, kTraceHwId, trace_hwreg_id());
+    trace_put(trace, kTraceItem, (blockIdx.x << 8) | blockIdx.y);
+    trace_put(trace, kTraceKind, kTraceCombineKind);
+    const int64_t w = (static_cast<int64_t>(blockIdx.y) * gridDim.x + blockIdx.x) *
+                          (kCombineThreads / kWave) + threadIdx.x / kWave;
+    a.trace[w * kWave + threadIdx.x % kWave] = trace;
+  }
+#endif
 }
 
 // ---------------------------------------------------------------------------
@@ -1003,10 +1039,9 @@ __global__ __launch_bounds__(kCombineThreads) void combine_kernel(CombineArgs a)
 // ---------------------------------------------------------------------------
 constexpr int kCombineRowsMaxItems = kCombineRows;   // 32
 // Below this many (request, query head) rows the four-workgroup kernel's
-// wider spread of loads wins over the row kernel's one wave per row
-// (measured, cold calls: B4 x 20K and B4 x 4K 1.7-1.8 us faster with four
-// workgroups per row, B8 0.4-1.3 us; from B16 the row kernel is 1.2-1.7 us
-// faster, B64 9 us, B256 38 us).
+// wider spread of loads wins over the row kernel's one wave per row (cold
+// calls: the four-workgroup kernel was faster up to B8, the row kernel from
+// B16 on, by more the larger the batch).
 #ifndef PG_COMBINE_ROWS_MIN_ROWS
 #define PG_COMBINE_ROWS_MIN_ROWS 512
 #endif
@@ -1129,7 +1164,13 @@ __global__ __launch_bounds__(kWave * kMaxWavesPerBlock) void decode_partial_kern
   HeadState st;
   init_state(st);
   PG_TRACE_MARK(st, kTraceStart);
+  // KV heads in blocks: workgroup y of an item reads the contiguous part
+  // y*W*128 .. (y+1)*W*128 of every token row (W waves per workgroup)
+#if PG_INTERLEAVED_HEADS
+  const int kv = wave * static_cast<int>(gridDim.y) + static_cast<int>(blockIdx.y);
+#else
   const int kv = blockIdx.y * a.waves_per_block + wave;
+#endif
   const WorkItem it = a.closed_form
                           ? closed_form_item(blockIdx.x, a.cf_items, a.cf_tail_items, a.cf_tail_begin,
                                              a.cf_tail_pages, a.cf_primary_begin, a.cf_primary_pages,
@@ -1518,6 +1559,12 @@ int32_t launch_combine(const pg_decode_plan_t* plan, const void* value_center,
     return check_launch("decode_combine");
   }
   const dim3 grid(rows, kHeadDim / 32);
+#if PG_TRACE
+  // combine rows follow the partial kernel's rows (one per wave of its grid)
+  const int64_t partial_words = static_cast<int64_t>(plan->num_items) * plan->num_kv_heads * kWave;
+  const int64_t combine_words = static_cast<int64_t>(grid.x) * grid.y * (kCombineThreads / kWave) * kWave;
+  c.trace = (partial_words + combine_words) * 4 <= g_trace_bytes ? g_trace + partial_words : nullptr;
+#endif
   if (stop_event) {
     hipExtLaunchKernelGGL(combine_kernel, grid, dim3(kCombineThreads), 0, as_stream(stream),
                           nullptr, static_cast<hipEvent_t>(stop_event), 0, c);

@@ -20,8 +20,8 @@ int64_t align_up(int64_t v, int64_t a) { return (v + a - 1) / a * a; }
 // KV heads (waves) per workgroup.  All of a page's heads in one workgroup
 // keep its 16 KiB of codes on one CU (the best layout once the items fill
 // most CUs); with fewer items the heads are split over several workgroups
-// so that every CU gets work (measured on MI355X: a 4K-token request, 64
-// items, runs 10.6 -> 7.6 us with two-wave workgroups).
+// so that every CU gets work (a 4K-token request: 64 items in two-wave
+// workgroups).
 int waves_per_block_for(int hkv, int64_t items, int64_t num_cus) {
   int w = kMaxWavesPerBlock;
   while (w > 1 && hkv % w) w >>= 1;
@@ -30,9 +30,8 @@ int waves_per_block_for(int hkv, int64_t items, int64_t num_cus) {
     // SIMD (the partial kernel's registers) one 8-wave workgroup fills a CU,
     // so each item's start-up and drain leave its CU idle.  Narrower
     // workgroups put two items on each CU that overlap each other's
-    // start-up (measured, cold kernels: B16 x 16K 139.7 -> 118.8 us, B64 x
-    // 8K 231.2 -> 211.5, B128 x 4K 225.6 -> 210.6, 256 ragged requests
-    // 264.8 -> 254.7); with at most one item per CU the width made no
+    // start-up (faster on every multi-round batch timed, B16 x 16K to 256
+    // ragged requests); with at most one item per CU the width made no
     // difference (B8 ragged, B1 128K).
     while (w > kMultiRoundWaves && hkv % (w >> 1) == 0) w >>= 1;
     return w;

@@ -108,3 +108,42 @@ def test_trace_summary_phases_per_xcd():
     assert out["end_at"]["max"] == pytest.approx(800 * tick)
     assert out["end_at_p50_by_xcc"] == {0: 8.0, 1: 8.0}
     assert out["waves_per_call"] == 2 and out["kernel_event_mean_us"] == 9.0
+
+
+def test_combine_trace_summary_boundary_per_xcd():
+    """The combine rows' arithmetic: per XCD, the boundary is the first
+    combine start minus the last partial end on that XCD (clocks of two
+    XCDs 5000 ticks apart), the sums and the end after them only from the
+    wave that writes the output (its sums mark is set)."""
+    partial = np.zeros((2, 64), dtype=np.int64)
+    combine = np.zeros((3, 64), dtype=np.int64)
+    for w, (xcc, base) in enumerate(((0, 0), (1, 5000))):
+        partial[w, bench.TRACE_XCC], partial[w, bench.TRACE_KIND] = xcc, 0
+        partial[w, bench.TRACE_START], partial[w, bench.TRACE_END] = base, base + 2000
+    for w, (xcc, base, sums) in enumerate(((0, 0, 2310), (0, 0, 0), (1, 5000, 2330))):
+        r = combine[w]
+        r[bench.TRACE_XCC], r[bench.TRACE_KIND] = xcc, bench.CTRACE_KIND
+        marks = {bench.TRACE_START: 2100, bench.CTRACE_META: 2200, bench.CTRACE_ROWS: 2250,
+                 bench.CTRACE_MAX: 2280, bench.CTRACE_END: 2400}
+        for lane, t in marks.items():
+            r[lane] = base + t
+        r[bench.CTRACE_SUMS] = base + sums if sums else 0
+    out = bench.combine_trace_summary([partial.astype(np.int32)], [combine.astype(np.int32)])
+    tick = bench.TRACE_TICK_US
+    assert out["boundary"]["p50"] == pytest.approx(100 * tick) and out["boundary"]["n"] == 2
+    assert out["meta_rtt"]["p50"] == pytest.approx(100 * tick)
+    assert out["rows_rtt"]["p50"] == pytest.approx(150 * tick)
+    assert out["max_after_rows"]["p50"] == pytest.approx(30 * tick)
+    assert out["sums_after_max"]["n"] == 2
+    assert out["sums_after_max"]["max"] == pytest.approx(50 * tick)
+    assert out["end_after_sums"]["p50"] == pytest.approx(80 * tick)   # 90 and 70 ticks
+    assert out["end_after_sums"]["max"] == pytest.approx(90 * tick)
+    assert out["wave_life"]["max"] == pytest.approx(300 * tick)
+    assert out["span"]["n"] == 2
+
+
+def test_combine_trace_summary_refuses_missing_rows():
+    partial = np.zeros((1, 64), dtype=np.int32)
+    combine = np.zeros((1, 64), dtype=np.int32)
+    with pytest.raises(RuntimeError, match="combine trace rows missing"):
+        bench.combine_trace_summary([partial], [combine])
