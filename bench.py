@@ -650,12 +650,19 @@ def decoder_config5(torch, device, repeats: int, context: int = 16384, steps: in
     kv_bytes["page_gauge_heterogeneous"] = kv_bytes["page_gauge"]
     weight_bytes = weights.bytes_per_token()
     logits = {}
-    for name, d in decoders.items():
+    names = list(decoders)
+    for d in decoders.values():
         d.generate(first, context, steps, use_graphs=True)          # capture + warm
-        torch.cuda.synchronize()
-        walls, gpu = [], []
-        tokens_ref = None
-        for _ in range(repeats):
+    torch.cuda.synchronize()
+    walls = {name: [] for name in names}
+    gpu = {name: [] for name in names}
+    tokens_ref = {}
+    # the decoders take turns, in a rotating order, so that a drift of the
+    # GPU's clocks or caches over the run does not favour one of them
+    for rep in range(repeats):
+        for k in range(len(names)):
+            name = names[(rep + k) % len(names)]
+            d = decoders[name]
             e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
             torch.cuda.synchronize()
             w0 = time.perf_counter()
@@ -663,29 +670,42 @@ def decoder_config5(torch, device, repeats: int, context: int = 16384, steps: in
             toks, _ = d.generate(first, context, steps, use_graphs=True)
             e1.record()
             torch.cuda.synchronize()
-            walls.append(time.perf_counter() - w0)
-            gpu.append(e0.elapsed_time(e1) * 1e-3)
-            tokens_ref = toks if tokens_ref is None else tokens_ref
-            if not torch.equal(toks, tokens_ref):
+            walls[name].append(time.perf_counter() - w0)
+            gpu[name].append(e0.elapsed_time(e1) * 1e-3)
+            tokens_ref.setdefault(name, toks)
+            if not torch.equal(toks, tokens_ref[name]):
                 raise RuntimeError("greedy decode is not deterministic across repeats")
-        # eager (no graph) once, for the launch-overhead comparison
+    # eager steps (no graph), timed the same way, for the launch-overhead
+    # comparison
+    eager = {name: [] for name in names}
+    for d in decoders.values():
         d.drop_graphs()
-        torch.cuda.synchronize()
-        w0 = time.perf_counter()
-        d.generate(first, context, steps, use_graphs=False)
-        torch.cuda.synchronize()
-        eager_s = time.perf_counter() - w0
-        ms_token = 1e3 * statistics.median(walls) / steps          # per decode step
+        d.generate(first, context, steps, use_graphs=False)         # warm
+    for rep in range(repeats):
+        for k in range(len(names)):
+            name = names[(rep + k) % len(names)]
+            torch.cuda.synchronize()
+            w0 = time.perf_counter()
+            toks, _ = decoders[name].generate(first, context, steps, use_graphs=False)
+            torch.cuda.synchronize()
+            eager[name].append(time.perf_counter() - w0)
+            if not torch.equal(toks, tokens_ref[name]):
+                raise RuntimeError("eager and graph greedy decodes differ")
+    for name in names:
+        d = decoders[name]
+        eager_s = statistics.median(eager[name])
+        ms_token = 1e3 * statistics.median(walls[name]) / steps          # per decode step
         total_bytes = weight_bytes + batch * kv_bytes[name]
         result[name] = {
             "ms_per_token_wall_p50": round(ms_token, 4),
-            "ms_per_token_gpu_p50": round(1e3 * statistics.median(gpu) / steps, 4),
+            "ms_per_token_gpu_p50": round(1e3 * statistics.median(gpu[name]) / steps, 4),
             "tokens_per_s": round(batch * 1e3 / ms_token, 2),
-            "eager_ms_per_token": round(1e3 * eager_s / steps, 3),
+            "eager_ms_per_token": round(1e3 * eager_s / steps, 4),
+            "eager_tokens_per_s": round(batch * steps / eager_s, 2),
             "bytes_per_token": total_bytes,
             "achieved_gbps": round(total_bytes / (ms_token * 1e-3) / 1e9, 1),
             "hbm_frac": round(total_bytes / (ms_token * 1e-3) / 1e9 / HBM_PEAK_GBPS, 4),
-            "greedy_tokens": [int(t) for t in tokens_ref.reshape(-1).tolist()],
+            "greedy_tokens": [int(t) for t in tokens_ref[name].reshape(-1).tolist()],
         }
         if logit_gate:                          # teacher-forced logits for the comparison
             logits[name] = [d.step(forced[i], context + i).clone() for i in range(steps)]
