@@ -1196,7 +1196,7 @@ def _trace_stats(values):
             "p90": round(float(q[2]), 2), "max": round(float(v.max()), 2), "n": int(v.size)}
 
 
-def trace_summary(rows_per_call, kernel_us):
+def trace_summary(rows_per_call, kernel_us, waves_per_block: int = 0):
     """Phase statistics (µs) of the per-wave trace rows of several calls.
 
     Times are relative to the first wave start on the same XCD in the same
@@ -1205,12 +1205,15 @@ def trace_summary(rows_per_call, kernel_us):
     kernel's own event duration allows as a real skew).  Per INT8
     wave: page-id round trip (ids - start), first group's data (K of group
     0 - its issue), and per group g: the wait for K (K[g] - done[g-1]), QK,
-    softmax and the wait for V (V[g] - K[g]), PV issue (done[g] - V[g])."""
+    softmax and the wait for V (V[g] - K[g]), PV issue (done[g] - V[g]).
+    With ``waves_per_block``, also the p50 of each wave slot of a workgroup
+    (KV head modulo the workgroup's waves): first issue after the page ids,
+    first K data, end."""
     import numpy as np
     agg = {k: [] for k in ("start_at", "ids_rtt", "ids_at", "issued_at", "first_k_after_issue",
                            "first_k_at", "k_wait", "qk_to_v", "pv", "group_span", "end_at",
                            "end_at_fp16", "end_at_int8_last_group")}
-    by_xcc = {}
+    by_xcc, by_slot = {}, {}
     for rows in rows_per_call:
         r = rows.astype(np.int64) & 0xFFFFFFFF
         xcc = r[:, TRACE_XCC] & 0xF
@@ -1244,7 +1247,18 @@ def trace_summary(rows_per_call, kernel_us):
             agg["end_at_int8_last_group"].append(d[n - 1])
         for x in np.unique(xcc):
             by_xcc.setdefault(int(x), []).extend(list(rel(TRACE_END)[xcc == x]))
+        if waves_per_block:
+            slot = (r[:, TRACE_ITEM] & 0xFF) % waves_per_block
+            for w in range(waves_per_block):
+                sel = int8 & (slot == w)
+                d = by_slot.setdefault(w, {"issue_after_ids": [], "first_k_at": [], "end_at": []})
+                d["issue_after_ids"] += list((rel(TRACE_ISSUED) - rel(TRACE_IDS))[sel])
+                d["first_k_at"] += list(rel(TRACE_K)[sel])
+                d["end_at"] += list(rel(TRACE_END)[sel])
     out = {k: _trace_stats(v) for k, v in agg.items()}
+    if waves_per_block:
+        out["p50_by_wave_slot"] = {w: {k: round(float(np.median(v)), 2) for k, v in d.items() if v}
+                                   for w, d in sorted(by_slot.items())}
     out["end_at_p50_by_xcc"] = {x: round(float(np.median(v)), 2) for x, v in sorted(by_xcc.items())}
     out["kernel_event_mean_us"] = round(float(np.mean(kernel_us)), 3)
     out["waves_per_call"] = int(rows_per_call[0].shape[0])
@@ -1291,7 +1305,8 @@ def combine_trace_summary(partial_per_call, combine_per_call):
 
 def phase_trace(torch, decode, workloads, device, scrub, calls: int, dump: str = ""):
     """Per-wave phase trace of the partial kernel (trace build loaded), cold
-    calls after the clean scrub, at B1/49K, 16K and 4K."""
+    calls after the clean scrub, at B1/49K, 16K, 4K and config 3 (B8 ragged,
+    first validation seed)."""
     from pagegauge_amd import _capi
 
     lib = _capi.library()
@@ -1301,7 +1316,10 @@ def phase_trace(torch, decode, workloads, device, scrub, calls: int, dump: str =
     cases = (("b1_49k", lambda: workloads.b1_49k(workloads.VALIDATION_SEEDS[0], device=device)),
              ("b1_16k", lambda: workloads.build_decode_workload([16384 + 16], workloads.VALIDATION_SEEDS[0],
                                                                 device=device)),
-             ("config1_4k", lambda: workloads.single_4k(workloads.VALIDATION_SEEDS[0], device=device)))
+             ("config1_4k", lambda: workloads.single_4k(workloads.VALIDATION_SEEDS[0], device=device)),
+             ("config3_b8_ragged", lambda: workloads.build_decode_workload(
+                 workloads.ragged_lengths(workloads.VALIDATION_SEEDS[0]), workloads.VALIDATION_SEEDS[0],
+                 device=device)))
     for name, make in cases:
         w = make()
         dec = decode.PageGaugeSegmentedDecode(torch.empty(64 << 20, dtype=torch.uint8, device=device))
@@ -1339,7 +1357,7 @@ def phase_trace(torch, decode, workloads, device, scrub, calls: int, dump: str =
             raw[f"{name}_kernel_us"] = np.asarray(kernel)
         result[name] = {"work_items": dec.num_work_items,
                         "waves_per_block": int(dec._state.plan.waves_per_block),
-                        **trace_summary(rows, kernel),
+                        **trace_summary(rows, kernel, int(dec._state.plan.waves_per_block)),
                         "combine": combine_trace_summary(rows, combine_rows)}
         del w, dec, bound, buf
         torch.cuda.empty_cache()
