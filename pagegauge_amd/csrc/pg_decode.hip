@@ -1291,10 +1291,27 @@ __global__ __launch_bounds__(kWave * kMaxWavesPerBlock) void tail_merge_kernel(T
   const int kv = blockIdx.y * a.waves_per_block + head_slot;
   HeadState st;
   init_state(st);
+  // The old state and the value center of this lane's 8 dims are loaded
+  // first, unconditionally (every sub-wave, only sub-wave 0 uses them), and
+  // consumed after the walk: loaded there, they were one more round trip
+  // at the end.
+  const int qh = kv * kGqa + (lane >> 4);
+  const int n = lane & 15;
+  const int64_t row = static_cast<int64_t>(request) * a.num_qo_heads + qh;
+  uint16_t* o = t.old_output + row * kHeadDim + 8 * n;
+  const uint16_t* c = t.value_center + request * t.center_batch_stride + kv * kHeadDim + 8 * n;
+  v4u old_bits = *reinterpret_cast<const v4u*>(o);
+  v4u center_bits = *reinterpret_cast<const v4u*>(c);
+  float old_lse = t.old_lse[row];
   const int begin = request * t.pages_per_request;
   const int end = begin + t.pages_per_request;
   fp16_pages<true>(a, request, t.exact_k, t.exact_v, t.page_indices, begin, end, end - 1,
                    t.last_len[request], kv, lane, lds_all + wave * kLdsPerWave, st, sub, t.subs);
+  // every wave waits for its early loads here, long after they arrived (a
+  // wave that leaves below does not leave with loads in flight)
+  consume_point(old_bits);
+  consume_point(center_bits);
+  consume_point(old_lse);
   if (t.subs > 1) {
     sub_state[wave][0][lane] = st.m;
     sub_state[wave][1][lane] = st.l;
@@ -1322,24 +1339,26 @@ __global__ __launch_bounds__(kWave * kMaxWavesPerBlock) void tail_merge_kernel(T
     for (int i = 0; i < 8; ++i) st.o[i] = o[i];
   }
   const float l_row = row16_sum(st.l);
-  const int qh = kv * kGqa + (lane >> 4);
-  const int n = lane & 15;
-  const int64_t row = static_cast<int64_t>(request) * a.num_qo_heads + qh;
-  const float old_lse = t.old_lse[row];
   const float mx = fmaxf(old_lse, st.m);
   const float w_old = (old_lse == kNegInf) ? 0.0f : exp2f(old_lse - mx);
   const float w_new = (st.m == kNegInf) ? 0.0f : exp2f(st.m - mx);
   const float den = w_old + w_new * l_row;
   const float inv = den > 0.0f ? 1.0f / den : 0.0f;
-  uint16_t* o = t.old_output + row * kHeadDim;
-  const uint16_t* c = t.value_center + request * t.center_batch_stride + kv * kHeadDim;
+  v4u merged_bits;
 #pragma unroll
-  for (int nb = 0; nb < 8; ++nb) {
-    const int d = 8 * n + nb;
-    const float merged = (w_old * half_bits_to_float(o[d]) + w_new * st.o[nb]) * inv +
-                         half_bits_to_float(c[d]);
-    o[d] = __half_as_ushort(__float2half_rn(merged));
+  for (int i = 0; i < 4; ++i) {
+    uint32_t word = 0;
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const int nb = 2 * i + h;
+      const float old_v = half_bits_to_float(static_cast<uint16_t>(old_bits[i] >> (16 * h)));
+      const float center = half_bits_to_float(static_cast<uint16_t>(center_bits[i] >> (16 * h)));
+      const float merged = (w_old * old_v + w_new * st.o[nb]) * inv + center;
+      word |= static_cast<uint32_t>(__half_as_ushort(__float2half_rn(merged))) << (16 * h);
+    }
+    merged_bits[i] = word;
   }
+  *reinterpret_cast<v4u*>(o) = merged_bits;
   if (n == 0) t.old_lse[row] = den > 0.0f ? log2f(den) + mx : kNegInf;
 }
 
