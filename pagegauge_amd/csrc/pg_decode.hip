@@ -701,6 +701,13 @@ __device__ __forceinline__ void fp16_pages(const DecodeArgs& a, int request, con
   // every lane reads its head's query row): a conditional load compiles to
   // a branch that waits for it before the next load can leave.
   const int my_page = indices[begin + min(lane, count - 1)];
+  // the decode step's position, when this pass finalizes a completed page:
+  // loaded here (from a valid address either way) and consumed at the last
+  // page, where a load would be one more round trip
+  const bool finalizing = a.finalize_positions != nullptr;
+  const int32_t* position_at =
+      finalizing ? a.finalize_positions + request * a.finalize_position_stride : indices + begin;
+  int finalize_position = *position_at;
 
   // Q operand: head h on row 4h; lanes of other rows hold zeros.
   v8h qa[4];
@@ -755,9 +762,10 @@ __device__ __forceinline__ void fp16_pages(const DecodeArgs& a, int request, con
     v4f acc = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
     for (int j = 0; j < 4; ++j) acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(qa[j], cur.k[j], acc, 0, 0, 0);
-    if (a.finalize_positions != nullptr && slot == last_slot) {
+    if (finalizing && slot == last_slot) {
       // the step's token completed this (the segment's last) page
-      const int position = a.finalize_positions[request * a.finalize_position_stride];
+      consume_point(finalize_position);
+      const int position = finalize_position;
       if (position >= 0 && position % kPageSize == kPageSize - 1 &&
           position / kPageSize < a.code_pages_per_request)
         finalize_page(a, request, position / kPageSize, kv, lane, cur.k, cur.v);
