@@ -311,7 +311,8 @@ __device__ __forceinline__ float softmax_update_fast(HeadState& st, const float 
 // ---------------------------------------------------------------------------
 template <int kRowStride>
 __device__ __forceinline__ void int8_chunk(const DecodeArgs& a, const WorkItem& it, int kv,
-                                           int lane, uint8_t* lds, HeadState& st) {
+                                           int lane, uint8_t* lds, HeadState& st,
+                                           const int* preloaded_page = nullptr) {
   const int hkv = a.num_kv_heads;
   const int m16 = lane & 15;
   const int kg = lane >> 4;
@@ -328,7 +329,13 @@ __device__ __forceinline__ void int8_chunk(const DecodeArgs& a, const WorkItem& 
   const int groups = (count + kGroupPages - 1) / kGroupPages;
 
   // Chunk metadata, one lane per page slot: physical page and K/V page scales.
-  const int my_page = a.indices[begin + min(lane, count - 1)];
+  // ``preloaded_page``: this lane's entry of a wider range starting at the
+  // same page, loaded by the caller before the chunk's end was known; lanes
+  // past the chunk take its last page by a select, as the clamp gives them.
+  const int my_page =
+      preloaded_page ? (lane < count ? *preloaded_page
+                                     : __builtin_amdgcn_readlane(*preloaded_page, count - 1))
+                     : a.indices[begin + min(lane, count - 1)];
 
   // ---- query (A operand of QK): dims 16*kg + 64*j + b, b = 0..15
   const uint16_t* q = a.query + it.request * a.query_batch_stride +
@@ -1193,16 +1200,19 @@ __global__ __launch_bounds__(kWave * kMaxWavesPerBlock) void decode_partial_kern
   } else if (it.kind == PG_KV_HETEROGENEOUS) {
     // One unified table: the request's first old_kv_len/16 pages are INT8
     // codes, the rest index the FP16 exact pages.  The boundary is read at run
-    // time; an item that straddles it runs both paths into one state.
+    // time; an item that straddles it runs both paths into one state.  The
+    // item's page ids leave with the boundary's load (not after it): the
+    // INT8 part takes its entries from them.
+    const int item_page = a.indices[it.page_begin + min(lane, it.page_end - it.page_begin - 1)];
     const int boundary = min(max(it.request_page_begin + a.old_kv_len[it.request] / kPageSize,
                                  it.page_begin), it.page_end);
     if (boundary > it.page_begin) {
       WorkItem old_part = it;
       old_part.page_end = boundary;
       if (a.num_kv_heads == 8)
-        int8_chunk<8 * kHeadDim>(a, old_part, kv, lane, lds, st);
+        int8_chunk<8 * kHeadDim>(a, old_part, kv, lane, lds, st, &item_page);
       else
-        int8_chunk<0>(a, old_part, kv, lane, lds, st);
+        int8_chunk<0>(a, old_part, kv, lane, lds, st, &item_page);
     }
     if (boundary < it.page_end)
       fp16_pages(a, it.request, a.tail_k, a.tail_v, a.indices, boundary, it.page_end, it.last_page,
