@@ -69,13 +69,16 @@ def test_variant_is_bit_identical_to_the_product(cuda, variant, lengths, split):
     assert torch.equal(out, out2) and torch.equal(lse, lse2)
 
 
-@pytest.mark.parametrize("lengths", [[16400], [720, 4096, 1008]])
+@pytest.mark.parametrize("lengths", [[16400], [720, 4096, 1008],
+                                     workloads.ragged_lengths(workloads.VALIDATION_SEEDS[0])])
 def test_trace_rows_with_the_buffer_set(cuda, lengths):
     """With a trace buffer, the trace build still returns the product's bits,
     and every wave of the partial kernel and (for the four-workgroup combine)
     of the combine kernel writes its row: a known XCD, and marks in the
     order the kernel reaches them (32-bit counter differences, which a wrap
-    of s_memrealtime leaves intact)."""
+    of s_memrealtime leaves intact).  Shapes: the medium plan (4-wave
+    workgroups), a small ragged batch, and config 3's B8 ragged batch (the
+    large plan's 8-wave workgroups)."""
     lib = _variant("trace")
     w, dec, out, lse = _product_and_plan(cuda, lengths, None)
     plan = dec._state.plan
@@ -94,6 +97,9 @@ def test_trace_rows_with_the_buffer_set(cuda, lengths):
     part, comb = rows[:partial_waves], rows[partial_waves:]
     after = lambda r, a, b: ((r[:, b] - r[:, a]) & 0xFFFFFFFF) < (1 << 31)   # noqa: E731
     assert np.all(part[:, 53] & 0xF < 8) and np.all(part[:, 56] != 100)
+    # one row per wave of the grid: every (item, KV head) exactly once
+    seen = sorted(int(x) for x in part[:, 55])
+    assert seen == sorted((i << 8) | h for i in range(plan.num_items) for h in range(8))
     assert np.all(after(part, 0, 52))                      # start .. end
     int8 = part[:, 56] == 0
     assert int8.any()
