@@ -24,7 +24,9 @@ digest of the sources and flags it was built from (``variant_is_current``):
 * ``default_scheduler``: the product with the decode source under LLVM's
   default machine scheduler instead of the memory-clause strategy;
 * ``interleaved_heads``: the KV heads of an item's two workgroups
-  interleaved (even, odd) instead of in blocks (0-3, 4-7).
+  interleaved (even, odd) instead of in blocks (0-3, 4-7);
+* ``full_line_k``: whole 128-byte K rows per load instruction, the MFMA
+  operand handed over by a DPP rotation.
 """
 
 from __future__ import annotations
@@ -79,6 +81,7 @@ VARIANTS = {
     # None: the source's own flags are dropped, not extended
     "default_scheduler": {"pg_decode.hip": None},
     "interleaved_heads": {"pg_decode.hip": ["-DPG_INTERLEAVED_HEADS=1"]},
+    "full_line_k": {"pg_decode.hip": ["-DPG_FULL_LINE_K=1"]},
 }
 
 

@@ -114,6 +114,12 @@ constexpr uint32_t kTraceCombineKind = 100;
 #ifndef PG_INTERLEAVED_HEADS
 #define PG_INTERLEAVED_HEADS 0
 #endif
+// Alternative build for the A/B: each K load instruction reads whole
+// 128-byte rows (8 rows per instruction) and a DPP rotation hands each lane
+// its MFMA operand, instead of 16 half rows per instruction.
+#ifndef PG_FULL_LINE_K
+#define PG_FULL_LINE_K 0
+#endif
 
 struct DecodeArgs {
   const uint16_t* query;
@@ -205,6 +211,20 @@ __device__ __forceinline__ uint32_t trace_hwreg_id() {
 #define PG_TRACE_AFTER(st, slot, loaded) ((void)0)
 #define PG_TRACE_PUT(st, slot, value) ((void)0)
 #endif
+
+// Full-line K loads (PG_FULL_LINE_K): lane m16 < 8 holds (own MFMA 0 data,
+// MFMA 0 data of lane m16 + 8), lane m16 >= 8 (MFMA 1 data of lane m16 - 8,
+// own MFMA 1 data); one 8-lane rotation within each 16-lane row sends each
+// lane the half its partner holds for it.
+__device__ __forceinline__ void swap_k_halves(v4i (&k)[2], bool upper) {
+#pragma unroll
+  for (int w = 0; w < 4; ++w) {
+    const int send = upper ? k[0][w] : k[1][w];
+    const int got = __builtin_amdgcn_mov_dpp(send, 0x128, 0xf, 0xf, false);   // row_ror:8
+    k[0][w] = upper ? got : k[0][w];
+    k[1][w] = upper ? k[1][w] : got;
+  }
+}
 
 // 4x4 byte transpose: r[k] holds 4 dims of token k; returns c[j] holding
 // dim j of tokens 0..3.  v_perm_b32(hi, lo, sel) picks byte sel_i of the
@@ -368,7 +388,17 @@ __device__ __forceinline__ void int8_chunk(const DecodeArgs& a, const WorkItem& 
   // the chunk end re-read its last page: their scores are masked to -inf and
   // their probabilities (hence digits) are zero.
   Int8Group buf[2];
+#if PG_FULL_LINE_K
+  // whole 128-byte K rows per instruction: the first load of a page takes
+  // rows 0-7 (lanes m16 < 8 their own dims 16kg.., lanes m16 >= 8 dims
+  // 64 + 16kg.. of row m16 - 8), the second rows 8-15; swap_k_halves then
+  // trades the halves between lanes 8 apart
+  const uint32_t k_off = static_cast<uint32_t>((m16 & 7) * row_stride + (m16 & 8) * 8 + 16 * kg);
+  const uint32_t k_off_second = static_cast<uint32_t>(k_off + 8 * row_stride);
+#else
   const uint32_t k_off = static_cast<uint32_t>(m16 * row_stride + 16 * kg);
+  const uint32_t k_off_second = k_off + 64;
+#endif
   const uint32_t v_off = static_cast<uint32_t>(4 * kg * row_stride + 8 * m16);
   auto issue = [&](int g, Int8Group& dst) {
     const int8_t* kp[kGroupPages];
@@ -382,7 +412,7 @@ __device__ __forceinline__ void int8_chunk(const DecodeArgs& a, const WorkItem& 
 #pragma unroll
     for (int i = 0; i < kGroupPages; ++i) {
       dst.k[i][0] = *reinterpret_cast<const v4i*>(kp[i] + k_off);
-      dst.k[i][1] = *reinterpret_cast<const v4i*>(kp[i] + k_off + 64);
+      dst.k[i][1] = *reinterpret_cast<const v4i*>(kp[i] + k_off_second);
     }
 #pragma unroll
     for (int i = 0; i < kGroupPages; ++i)
@@ -496,6 +526,10 @@ __device__ __forceinline__ void int8_chunk(const DecodeArgs& a, const WorkItem& 
       consume_point(cur.k[i][1]);
     }
     if (PG_TRACE && g < kTraceSlots) PG_TRACE_AFTER(st, kTraceK + g, cur.k[kGroupPages - 1][1][3]);
+#if PG_FULL_LINE_K
+#pragma unroll
+    for (int i = 0; i < kGroupPages; ++i) swap_k_halves(cur.k[i], m16 >= 8);
+#endif
     // ---- QK: exact integer dot products
     float s[kGroupPages];
     float svu[kGroupPages];

@@ -6,6 +6,7 @@ comparison) must compute the product's decode outputs bit for bit:
   the same integer query digits as the product's i8 MFMA;
 * ``default_scheduler``: the same source under LLVM's default scheduler;
 * ``interleaved_heads``: an item's workgroups take interleaved KV heads;
+* ``full_line_k``: whole-row K loads and a DPP hand-over of the MFMA operand;
 * ``trace``, ``trace_conditional_scales``: the phase-trace builds, with and
   without a trace buffer set (with one, every wave of both kernels writes a
   row, checked for the marks' order).
@@ -58,7 +59,7 @@ def _product_and_plan(cuda, lengths, split):
 
 
 @pytest.mark.parametrize("variant", ["qk_valu", "default_scheduler", "interleaved_heads", "trace",
-                                     "trace_conditional_scales"])
+                                     "trace_conditional_scales", "full_line_k"])
 @pytest.mark.parametrize("lengths,split", CASES)
 def test_variant_is_bit_identical_to_the_product(cuda, variant, lengths, split):
     lib = _variant(variant)
