@@ -86,6 +86,22 @@ def test_medium_plans_with_long_items(cuda, workspace, lengths):
     assert max_abs(lse, ref_lse) <= LSE_TOL
 
 
+def test_large_plan_one_request(cuda, workspace):
+    """One request past 30 weighted pages per CU (128K tokens: 8192 INT8
+    pages + the 16-page ring): the large plan's one-round items in 8-wave
+    workgroups, described in closed form (no work-item loads)."""
+    from pagegauge_amd import workloads
+
+    w = workloads.build_decode_workload([131072 + 256], seed=20260842, device=cuda)
+    out, lse, dec = _segmented(w, workspace)
+    plan = dec._state.plan
+    print("large B1", plan.num_items, plan.waves_per_block, plan.closed_form, flush=True)
+    assert plan.waves_per_block == 8 and plan.closed_form == 1 and plan.num_items <= 256
+    ref_out, ref_lse, _ = oracle_decode(w)
+    assert max_abs(out, ref_out) <= OUT_TOL
+    assert max_abs(lse, ref_lse) <= LSE_TOL
+
+
 @pytest.mark.parametrize("flat,code", [("query", 127), ("query", -127), ("keys", 127)])
 def test_pv_digits_of_64_page_items_at_the_accumulator_bound(cuda, workspace, flat, code):
     """Adversarial 64-page INT8 items (16 PV groups without a fold).
