@@ -196,3 +196,37 @@ def test_heterogeneous_run_validation(cuda):
     with pytest.raises(RuntimeError, match="plan"):
         wrapper.run(d["query"], (d["k_codes"], d["v_codes"]), d["k_scale"], d["v_scale"],
                     d["exact_k"], d["exact_v"], d["old_len"], d["center"])
+
+
+@pytest.mark.parametrize("lengths", [[49152], [20480] * 4])
+def test_hinted_heterogeneous_is_bit_identical_to_segmented(cuda, lengths):
+    """With the exact-tail hint of the ring's 16 pages the unified-table plan
+    cuts the same items as the segmented plan (config 2's B1/49K and the
+    paper's B4 x 20K shape), so the two calls return the same bits: the
+    heterogeneous items take their INT8 pages and page ids exactly as the
+    segmented INT8 items do."""
+    from pagegauge_amd import decode, workloads
+
+    w = workloads.build_decode_workload(lengths, 20260840, device=cuda)
+    seg = decode.PageGaugeSegmentedDecode(torch.empty(64 << 20, dtype=torch.uint8, device=cuda))
+    seg.plan(w.old_indptr, w.old_indices, w.old_last_page_len, w.tail_indptr, w.tail_indices,
+             w.tail_last_page_len)
+    out_s, lse_s = seg.run(w.query, (w.k_codes, w.v_codes), w.k_scale, w.v_scale,
+                           (w.tail_k, w.tail_v), w.value_center, return_lse=True)
+    old_ptr, tail_ptr = w.old_indptr.tolist(), w.tail_indptr.tolist()
+    old_idx, tail_idx = w.old_indices.cpu(), w.tail_indices.cpu()
+    rows, indptr, old_len = [], [0], []
+    for b in range(w.batch):
+        rows += [old_idx[old_ptr[b]:old_ptr[b + 1]], tail_idx[tail_ptr[b]:tail_ptr[b + 1]]]
+        indptr.append(indptr[-1] + old_ptr[b + 1] - old_ptr[b] + tail_ptr[b + 1] - tail_ptr[b])
+        old_len.append(16 * (old_ptr[b + 1] - old_ptr[b]))
+    unified = torch.cat(rows).to(cuda)
+    het = decode.make_heterogeneous_page_gauge_wrapper(
+        None, torch.empty(64 << 20, dtype=torch.uint8, device=cuda))
+    het.plan(torch.tensor(indptr, dtype=torch.int32), unified, w.tail_last_page_len, 32, 8, 128, 16,
+             exact_tail_pages_hint=16)
+    out_h, lse_h = het.run(w.query, (w.k_codes, w.v_codes), w.k_scale, w.v_scale, w.tail_k,
+                           w.tail_v, torch.tensor(old_len, dtype=torch.int32, device=cuda),
+                           w.value_center, return_lse=True)
+    torch.cuda.synchronize()
+    assert torch.equal(out_h, out_s) and torch.equal(lse_h, lse_s)
