@@ -57,13 +57,16 @@ int32_t pg_probe_decode_walk(const void* k_pages, const void* v_pages, const int
                              void* start_event, void* stop_event, void* stream);
 
 /* ------------------------------------------------------------------------
- * Phase trace of the decode partial kernel.  Exported only by the trace
- * build of the product library (python -m pagegauge_amd.build --variant
- * trace), not by libpagegauge_bench.so: sets the device buffer the partial
- * kernel writes one 64-word row per wave into (s_memrealtime marks of the
- * wave's start, page-id arrival, first loads issued, scale arrival, each
- * group's K and V arrival, end; XCC and HW_ID registers).  A launch whose
- * grid needs more than ``bytes`` writes no rows; NULL turns the trace off.
+ * Phase trace of the decode kernels.  Exported only by the trace builds of
+ * the product library (python -m pagegauge_amd.build --variant trace), not
+ * by libpagegauge_bench.so: sets the device buffer the partial kernel
+ * writes one 64-word row per wave into (s_memrealtime marks of the wave's
+ * start, page-id arrival, first loads issued, scale arrival, each group's K
+ * and V arrival, end; XCC and HW_ID registers), followed by one row per
+ * wave of the four-workgroup combine kernel (start, value center and item
+ * range arrival, partial rows arrival, maximum, sums, end; lane 56 holds
+ * 100).  A launch whose rows do not fit in ``bytes`` writes none; NULL
+ * turns the trace off.
  * ---------------------------------------------------------------------- */
 int32_t pg_trace_set_buffer(void* device_words, int64_t bytes);
 
